@@ -1,0 +1,372 @@
+// Packed-KV codec kernels: whole-prefix dequant, gather of selected entries, and the
+// 4-bit quantizers of the append path.  All integer/byte work, bit-exact against the
+// reference's torch codec (reference.py:35-268).
+#include "ma_common.h"
+
+namespace {
+
+constexpr int KG = 32;  // key token group (the only one shipped configs use)
+constexpr int VG = 32;  // value channel group
+
+struct PrefixArgs {
+    const uint8_t *kq;
+    const uint16_t *ks, *kz;
+    const uint8_t *vq;
+    const uint16_t *vs, *vz;
+    const void *kf, *vf;
+    int64_t skq[4], sks[3], svq[4], svs[3], skf[3], svf[3];
+    int nq, nf, fdtype;
+};
+
+PrefixArgs make_args(const ma_prefix *p) {
+    PrefixArgs a;
+    a.kq = (const uint8_t *)p->kq;
+    a.ks = (const uint16_t *)p->ks;
+    a.kz = (const uint16_t *)p->kz;
+    a.vq = (const uint8_t *)p->vq;
+    a.vs = (const uint16_t *)p->vs;
+    a.vz = (const uint16_t *)p->vz;
+    a.kf = p->kf;
+    a.vf = p->vf;
+    for (int i = 0; i < 4; ++i) {
+        a.skq[i] = p->skq[i];
+        a.svq[i] = p->svq[i];
+    }
+    for (int i = 0; i < 3; ++i) {
+        a.sks[i] = p->sks[i];
+        a.svs[i] = p->svs[i];
+        a.skf[i] = p->skf[i];
+        a.svf[i] = p->svf[i];
+    }
+    a.nq = p->nq;
+    a.nf = p->nf;
+    a.fdtype = p->fdtype;
+    return a;
+}
+
+// Dequantized key element (token j < nq, channel d) of lane (b, h).
+__device__ __forceinline__ float key_elem(const PrefixArgs &a, int b, int h, int j, int d) {
+    int g = j / KG, tt = j % KG;
+    const uint8_t *row = a.kq + b * a.skq[0] + h * a.skq[1] + (int64_t)g * a.skq[2] + (int64_t)d * a.skq[3];
+    uint32_t byte = row[tt >> 1];
+    uint32_t code = (tt & 1) ? (byte >> 4) : (byte & 15u);
+    int64_t so = b * a.sks[0] + h * a.sks[1] + (int64_t)g * a.sks[2] + d;
+    return ma_dq(code, ma_f16_to_f32(a.ks[so]), ma_f16_to_f32(a.kz[so]));
+}
+
+// ---------------------------------------------------------------- dequant_prefix
+// grid (ceil(n/64), B*H), 256 threads; one tile = 64 tokens x D channels of K and V.
+__global__ void __launch_bounds__(256) dequant_prefix_kernel(PrefixArgs a, int H, int D, ma_tensor4 ko,
+                                                             ma_tensor4 vo) {
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int n0 = blockIdx.x * 64;
+    const int n = a.nq + a.nf;
+    const int tid = threadIdx.x;
+    const int ncg = D / VG;
+
+    // keys, packed part: item = (group in tile, channel)
+    for (int it = tid; it < 2 * D; it += 256) {
+        int gl = it / D, d = it % D;
+        int t0 = n0 + gl * KG;
+        if (t0 >= a.nq) continue;
+        int g = t0 / KG;
+        const uint8_t *row = a.kq + b * a.skq[0] + h * a.skq[1] + (int64_t)g * a.skq[2] + (int64_t)d * a.skq[3];
+        uint4 raw = *(const uint4 *)row;
+        uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        int64_t so = b * a.sks[0] + h * a.sks[1] + (int64_t)g * a.sks[2] + d;
+        float sc = ma_f16_to_f32(a.ks[so]), zp = ma_f16_to_f32(a.kz[so]);
+        int64_t ob = b * ko.s[0] + h * ko.s[1] + d;
+#pragma unroll
+        for (int t = 0; t < KG; ++t) {
+            uint32_t code = (w[t >> 3] >> ((t & 7) * 4)) & 15u;
+            ma_store_f(ko.ptr, ob + (int64_t)(t0 + t) * ko.s[2], ko.dtype, ma_dq(code, sc, zp));
+        }
+    }
+    // values, packed part: item = (token, channel group)
+    for (int it = tid; it < 64 * ncg; it += 256) {
+        int tl = it / ncg, cg = it % ncg;
+        int j = n0 + tl;
+        if (j >= a.nq) continue;
+        const uint8_t *src = a.vq + b * a.svq[0] + h * a.svq[1] + (int64_t)j * a.svq[2] + (int64_t)cg * a.svq[3];
+        uint4 raw = *(const uint4 *)src;
+        uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        int64_t so = b * a.svs[0] + h * a.svs[1] + (int64_t)j * a.svs[2] + cg;
+        float sc = ma_f16_to_f32(a.vs[so]), zp = ma_f16_to_f32(a.vz[so]);
+        int64_t ob = b * vo.s[0] + h * vo.s[1] + (int64_t)j * vo.s[2] + cg * VG;
+#pragma unroll
+        for (int c = 0; c < VG; ++c) {
+            uint32_t code = (w[c >> 3] >> ((c & 7) * 4)) & 15u;
+            ma_store_f(vo.ptr, ob + c, vo.dtype, ma_dq(code, sc, zp));
+        }
+    }
+    // 16-bit part (residual tail, or the whole prefix of a bf16 cache)
+    for (int it = tid; it < 64 * D; it += 256) {
+        int tl = it / D, d = it % D;
+        int j = n0 + tl;
+        if (j < a.nq || j >= n) continue;
+        int jf = j - a.nq;
+        float kx = ma_load_f(a.kf, b * a.skf[0] + h * a.skf[1] + (int64_t)jf * a.skf[2] + d, a.fdtype);
+        float vx = ma_load_f(a.vf, b * a.svf[0] + h * a.svf[1] + (int64_t)jf * a.svf[2] + d, a.fdtype);
+        ma_store_f(ko.ptr, b * ko.s[0] + h * ko.s[1] + (int64_t)j * ko.s[2] + d, ko.dtype, kx);
+        ma_store_f(vo.ptr, b * vo.s[0] + h * vo.s[1] + (int64_t)j * vo.s[2] + d, vo.dtype, vx);
+    }
+}
+
+// ---------------------------------------------------------------- gather
+// grid (ceil(k / TPB_TOK), B*H), 256 threads; D/4 threads per selected entry, 4
+// channels each.  Indices outside [0, n) produce zeros (never an out-of-bounds read).
+__global__ void __launch_bounds__(256) gather_kernel(PrefixArgs a, int H, int D, const int64_t *idx, int64_t sib,
+                                                     int64_t sih, int k, ma_tensor4 ko, ma_tensor4 vo) {
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int tpt = D / 4;               // threads per token
+    const int toks = 256 / tpt;
+    const int i = blockIdx.x * toks + threadIdx.x / tpt;
+    const int c0 = (threadIdx.x % tpt) * 4;
+    if (i >= k) return;
+    const int n = a.nq + a.nf;
+    const int64_t j64 = idx[b * sib + h * sih + i];
+    float kx[4] = {0.f, 0.f, 0.f, 0.f}, vx[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j64 >= 0 && j64 < n) {
+        const int j = (int)j64;
+        if (j < a.nq) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kx[e] = key_elem(a, b, h, j, c0 + e);
+            const int cg = c0 / VG, w = c0 % VG;
+            const uint8_t *src = a.vq + b * a.svq[0] + h * a.svq[1] + (int64_t)j * a.svq[2] + (int64_t)cg * a.svq[3];
+            uint32_t two = (uint32_t)src[w >> 1] | ((uint32_t)src[(w >> 1) + 1] << 8);
+            int64_t so = b * a.svs[0] + h * a.svs[1] + (int64_t)j * a.svs[2] + cg;
+            float sc = ma_f16_to_f32(a.vs[so]), zp = ma_f16_to_f32(a.vz[so]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vx[e] = ma_dq((two >> (4 * e)) & 15u, sc, zp);
+        } else {
+            const int jf = j - a.nq;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kx[e] = ma_load_f(a.kf, b * a.skf[0] + h * a.skf[1] + (int64_t)jf * a.skf[2] + c0 + e, a.fdtype);
+                vx[e] = ma_load_f(a.vf, b * a.svf[0] + h * a.svf[1] + (int64_t)jf * a.svf[2] + c0 + e, a.fdtype);
+            }
+        }
+    }
+    const int64_t ok = b * ko.s[0] + h * ko.s[1] + (int64_t)i * ko.s[2] + c0;
+    const int64_t ov = b * vo.s[0] + h * vo.s[1] + (int64_t)i * vo.s[2] + c0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        ma_store_f(ko.ptr, ok + e, ko.dtype, kx[e]);
+        ma_store_f(vo.ptr, ov + e, vo.dtype, vx[e]);
+    }
+}
+
+// ---------------------------------------------------------------- quantizers
+// Arithmetic "in the source dtype": every op computed in f32 and rounded to the source
+// type, which is how torch's CPU kernels evaluate bf16/f16 tensors (reference.py:78-81).
+__device__ __forceinline__ float rnd(float x, int dtype) {
+    if (dtype == MA_BF16) return ma_round_bf16(x);
+    if (dtype == MA_F16) return ma_round_f16(x);
+    return x;
+}
+
+struct QuantGroup {
+    float lo, step;
+};
+
+__device__ __forceinline__ QuantGroup quant_params(float lo, float hi, int dtype) {
+    float step = rnd(rnd(hi - lo, dtype) / 15.0f, dtype);
+    step = rnd(fmaxf(step, 1e-8f), dtype);
+    return {lo, step};
+}
+
+__device__ __forceinline__ uint32_t quant_code(float x, QuantGroup q, int dtype) {
+    float r = rnd(rnd(x - q.lo, dtype) / q.step, dtype);
+    float c = __builtin_rintf(r);  // half to even
+    c = fminf(fmaxf(c, 0.0f), 15.0f);
+    return (uint32_t)c;
+}
+
+// keys: grid (T/KG, B*H), D threads; thread = one channel of one token group.
+__global__ void quantize_keys_kernel(ma_tensor4 src, int H, int D, uint8_t *kq, int64_t q0, int64_t q1, int64_t q2,
+                                     int64_t q3, _Float16 *ks, _Float16 *kz, int64_t s0, int64_t s1, int64_t s2) {
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int g = blockIdx.x;
+    const int d = threadIdx.x;
+    if (d >= D) return;
+    float x[KG];
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < KG; ++t) {
+        x[t] = ma_load_f(src.ptr, b * src.s[0] + h * src.s[1] + (int64_t)(g * KG + t) * src.s[2] + d, src.dtype);
+        lo = fminf(lo, x[t]);
+        hi = fmaxf(hi, x[t]);
+    }
+    QuantGroup qp = quant_params(lo, hi, src.dtype);
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < KG; ++t) w[t >> 3] |= quant_code(x[t], qp, src.dtype) << ((t & 7) * 4);
+    uint4 out = {w[0], w[1], w[2], w[3]};
+    *(uint4 *)(kq + b * q0 + h * q1 + (int64_t)g * q2 + (int64_t)d * q3) = out;
+    int64_t so = b * s0 + h * s1 + (int64_t)g * s2 + d;
+    ks[so] = (_Float16)qp.step;
+    kz[so] = (_Float16)qp.lo;
+}
+
+// values: one thread per (token, channel group); grid-stride over B*H*T*(D/VG) items.
+__global__ void __launch_bounds__(256) quantize_values_kernel(ma_tensor4 src, int BH, int H, int T, int D, uint8_t *vq,
+                                                              int64_t q0, int64_t q1, int64_t q2, int64_t q3,
+                                                              _Float16 *vs, _Float16 *vz, int64_t s0, int64_t s1,
+                                                              int64_t s2) {
+    const int ncg = D / VG;
+    const int64_t total = (int64_t)BH * T * ncg;
+    for (int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x; it < total; it += (int64_t)gridDim.x * 256) {
+        int cg = (int)(it % ncg);
+        int64_t rest = it / ncg;
+        int j = (int)(rest % T);
+        int bh = (int)(rest / T), b = bh / H, h = bh % H;
+        float x[VG];
+        float lo = INFINITY, hi = -INFINITY;
+        int64_t base = b * src.s[0] + h * src.s[1] + (int64_t)j * src.s[2] + cg * VG;
+#pragma unroll
+        for (int c = 0; c < VG; ++c) {
+            x[c] = ma_load_f(src.ptr, base + c, src.dtype);
+            lo = fminf(lo, x[c]);
+            hi = fmaxf(hi, x[c]);
+        }
+        QuantGroup qp = quant_params(lo, hi, src.dtype);
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < VG; ++c) w[c >> 3] |= quant_code(x[c], qp, src.dtype) << ((c & 7) * 4);
+        uint4 out = {w[0], w[1], w[2], w[3]};
+        *(uint4 *)(vq + b * q0 + h * q1 + (int64_t)j * q2 + (int64_t)cg * q3) = out;
+        int64_t so = b * s0 + h * s1 + (int64_t)j * s2 + cg;
+        vs[so] = (_Float16)qp.step;
+        vz[so] = (_Float16)qp.lo;
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- validation helpers
+int ma_validate_prefix(const ma_prefix *p, int D, const char *who) {
+    if (!p) {
+        ma_set_error("%s: prefix is NULL", who);
+        return MA_EINVAL;
+    }
+    if (D != 64 && D != 128) {
+        ma_set_error("%s: head_dim %d not built (64, 128)", who, D);
+        return MA_EUNSUPPORTED;
+    }
+    if (p->nq < 0 || p->nf < 0) {
+        ma_set_error("%s: negative prefix length", who);
+        return MA_EINVAL;
+    }
+    if (p->nq > 0) {
+        if (p->kbits != 4 || p->vbits != 4) {
+            ma_set_error("%s: packed bit widths k=%d v=%d not built (4/4)", who, p->kbits, p->vbits);
+            return MA_EUNSUPPORTED;
+        }
+        if (p->kgroup != KG || p->vgroup != VG) {
+            ma_set_error("%s: groups k=%d v=%d not built (32/32)", who, p->kgroup, p->vgroup);
+            return MA_EUNSUPPORTED;
+        }
+        if (p->nq % KG) {
+            ma_set_error("%s: quantized length %d is not a multiple of %d", who, p->nq, KG);
+            return MA_EINVAL;
+        }
+        if (!p->kq || !p->ks || !p->kz || !p->vq || !p->vs || !p->vz) {
+            ma_set_error("%s: packed prefix pointers missing", who);
+            return MA_EINVAL;
+        }
+        if ((((uintptr_t)p->kq | (uintptr_t)p->vq) & 15) || ((p->skq[2] | p->skq[3] | p->svq[2] | p->svq[3]) & 15)) {
+            ma_set_error("%s: packed payload rows must be 16-byte aligned", who);
+            return MA_EINVAL;
+        }
+        // key scale/zero are read as f16 pairs (two channels per 32-bit load)
+        if ((((uintptr_t)p->ks | (uintptr_t)p->kz) & 3) || ((p->sks[0] | p->sks[1] | p->sks[2]) & 1)) {
+            ma_set_error("%s: key scale/zero must be 4-byte aligned with even strides", who);
+            return MA_EINVAL;
+        }
+    }
+    if (p->nf > 0) {
+        if (!p->kf || !p->vf) {
+            ma_set_error("%s: 16-bit prefix pointers missing", who);
+            return MA_EINVAL;
+        }
+        if (p->fdtype != MA_BF16 && p->fdtype != MA_F16 && p->fdtype != MA_F32) {
+            ma_set_error("%s: bad prefix dtype %d", who, p->fdtype);
+            return MA_EINVAL;
+        }
+    }
+    return MA_OK;
+}
+
+static bool out_dtype_ok(int dt) { return dt == MA_BF16 || dt == MA_F32 || dt == MA_F16; }
+
+extern "C" int ma_dequant_prefix(const ma_prefix *p, int B, int H, int D, ma_tensor4 k_out, ma_tensor4 v_out,
+                                 void *stream) {
+    int rc = ma_validate_prefix(p, D, "ma_dequant_prefix");
+    if (rc) return rc;
+    if (B <= 0 || H <= 0 || !k_out.ptr || !v_out.ptr || !out_dtype_ok(k_out.dtype) || !out_dtype_ok(v_out.dtype)) {
+        ma_set_error("ma_dequant_prefix: bad sizes or outputs");
+        return MA_EINVAL;
+    }
+    int n = p->nq + p->nf;
+    if (n == 0) return MA_OK;
+    dim3 grid((n + 63) / 64, B * H);
+    hipLaunchKernelGGL(dequant_prefix_kernel, grid, dim3(256), 0, (hipStream_t)stream, make_args(p), H, D, k_out,
+                       v_out);
+    return ma_check_launch("ma_dequant_prefix");
+}
+
+extern "C" int ma_gather_kv(const ma_prefix *p, int B, int H, int D, const int64_t *idx, const int64_t sidx[2], int k,
+                            ma_tensor4 k_out, ma_tensor4 v_out, void *stream) {
+    int rc = ma_validate_prefix(p, D, "ma_gather_kv");
+    if (rc) return rc;
+    if (B <= 0 || H <= 0 || k < 0 || !idx || !sidx || !k_out.ptr || !v_out.ptr || !out_dtype_ok(k_out.dtype) ||
+        !out_dtype_ok(v_out.dtype)) {
+        ma_set_error("ma_gather_kv: bad sizes or outputs");
+        return MA_EINVAL;
+    }
+    if (k == 0) return MA_OK;
+    int toks = 256 / (D / 4);
+    dim3 grid((k + toks - 1) / toks, B * H);
+    hipLaunchKernelGGL(gather_kernel, grid, dim3(256), 0, (hipStream_t)stream, make_args(p), H, D, idx, sidx[0],
+                       sidx[1], k, k_out, v_out);
+    return ma_check_launch("ma_gather_kv");
+}
+
+extern "C" int ma_quantize_keys(ma_tensor4 src, int B, int H, int T, int D, int group, void *kq, const int64_t skq[4],
+                                void *ks, void *kz, const int64_t sks[3], void *stream) {
+    if (group != KG) {
+        ma_set_error("ma_quantize_keys: token group %d not built (32)", group);
+        return MA_EUNSUPPORTED;
+    }
+    if (B <= 0 || H <= 0 || T < 0 || T % KG || D <= 0 || D > 1024 || !src.ptr || !kq || !ks || !kz || !skq || !sks ||
+        ((uintptr_t)kq & 15) || ((skq[2] | skq[3]) & 15) || !out_dtype_ok(src.dtype)) {
+        ma_set_error("ma_quantize_keys: bad geometry (T %% 32, 16-byte aligned payload rows)");
+        return MA_EINVAL;
+    }
+    if (T == 0) return MA_OK;
+    dim3 grid(T / KG, B * H);
+    hipLaunchKernelGGL(quantize_keys_kernel, grid, dim3(D), 0, (hipStream_t)stream, src, H, D, (uint8_t *)kq, skq[0],
+                       skq[1], skq[2], skq[3], (_Float16 *)ks, (_Float16 *)kz, sks[0], sks[1], sks[2]);
+    return ma_check_launch("ma_quantize_keys");
+}
+
+extern "C" int ma_quantize_values(ma_tensor4 src, int B, int H, int T, int D, int group, void *vq,
+                                  const int64_t svq[4], void *vs, void *vz, const int64_t svs[3], void *stream) {
+    if (group != VG) {
+        ma_set_error("ma_quantize_values: channel group %d not built (32)", group);
+        return MA_EUNSUPPORTED;
+    }
+    if (B <= 0 || H <= 0 || T < 0 || D <= 0 || D % VG || !src.ptr || !vq || !vs || !vz || !svq || !svs ||
+        ((uintptr_t)vq & 15) || ((svq[2] | svq[3]) & 15) || !out_dtype_ok(src.dtype)) {
+        ma_set_error("ma_quantize_values: bad geometry (D %% 32, 16-byte aligned payload rows)");
+        return MA_EINVAL;
+    }
+    if (T == 0) return MA_OK;
+    int64_t items = (int64_t)B * H * T * (D / VG);
+    int blocks = (int)((items + 255) / 256);
+    if (blocks > 65535) blocks = 65535;
+    hipLaunchKernelGGL(quantize_values_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, src, B * H, H, T, D,
+                       (uint8_t *)vq, svq[0], svq[1], svq[2], svq[3], (_Float16 *)vs, (_Float16 *)vz, svs[0], svs[1],
+                       svs[2]);
+    return ma_check_launch("ma_quantize_values");
+}

@@ -1,0 +1,129 @@
+// Shared device helpers for the gfx950 kernels of libmaskahead_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "maskahead_hip.h"
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+#define MA_WAVE 64
+
+// ---- host-side error reporting (ma_runtime.cpp)
+void ma_set_error(const char *fmt, ...);
+int ma_check_launch(const char *what);
+int ma_num_cus();
+
+// ---- scalar conversions
+__device__ __forceinline__ float ma_f16_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ float ma_bf16_to_f32(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+// round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint16_t ma_f32_to_bf16(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t ma_pack_bf16x2(float lo, float hi) {
+    bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float ma_round_bf16(float f) {
+    return ma_bf16_to_f32(ma_f32_to_bf16(f));
+}
+__device__ __forceinline__ float ma_round_f16(float f) {
+    return (float)(_Float16)f;
+}
+
+// load one element of a 16/32-bit float tensor as f32
+__device__ __forceinline__ float ma_load_f(const void *base, int64_t off, int dtype) {
+    if (dtype == MA_BF16) return ma_bf16_to_f32(((const uint16_t *)base)[off]);
+    if (dtype == MA_F16) return ma_f16_to_f32(((const uint16_t *)base)[off]);
+    return ((const float *)base)[off];
+}
+__device__ __forceinline__ void ma_store_f(void *base, int64_t off, int dtype, float v) {
+    if (dtype == MA_BF16) ((uint16_t *)base)[off] = ma_f32_to_bf16(v);
+    else if (dtype == MA_F16) ((_Float16 *)base)[off] = (_Float16)v;
+    else ((float *)base)[off] = v;
+}
+
+// 8 consecutive elements of a float tensor, converted to bf16 (16-byte aligned for 16-bit
+// dtypes when off is a multiple of 8)
+__device__ __forceinline__ bf16x8_t ma_load8_as_bf16(const void *base, int64_t off, int dtype) {
+    if (dtype == MA_BF16) {
+        return *(const bf16x8_t *)((const uint16_t *)base + off);
+    }
+    bf16x8_t r;
+    if (dtype == MA_F16) {
+        typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+        f16x8_t h = *(const f16x8_t *)((const uint16_t *)base + off);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = (__bf16)(float)h[i];
+    } else {
+        const f32x4_t *p = (const f32x4_t *)((const float *)base + off);
+        f32x4_t a = p[0], b = p[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r[i] = (__bf16)a[i];
+            r[4 + i] = (__bf16)b[i];
+        }
+    }
+    return r;
+}
+
+// x = f32(code) * f32(scale) + f32(zero); the product is exact, so fused or not the
+// result carries one rounding -- bit-identical to the reference's two torch ops.
+__device__ __forceinline__ float ma_dq(uint32_t code, float scale, float zero) {
+    return __builtin_fmaf((float)code, scale, zero);
+}
+
+// ---- wave reductions (64 lanes)
+__device__ __forceinline__ float ma_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float ma_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ int ma_wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Combine a lane's value with that of its partner lane l ^ 32 (v_permlane32_swap on
+// gfx950 exchanges the upper half of one copy with the lower half of the other, so the
+// two results hold {own, partner} in some order; max and + are symmetric, and IEEE
+// addition is commutative, so both lanes of a pair get bit-identical results).
+__device__ __forceinline__ float ma_max_xor32(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float ma_sum_xor32(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ f32x16_t ma_mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---- monotone float key for selection: larger float -> larger key; -0.0 == +0.0;
+// NaN above +inf (torch.topk ranks NaN first)
+__device__ __forceinline__ uint32_t ma_order_key(float f) {
+    if (f != f) return 0xffffffffu;
+    if (f == 0.0f) f = 0.0f;
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+#define MA_LOG2E 1.4426950408889634f

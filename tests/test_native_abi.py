@@ -1,0 +1,68 @@
+"""The C ABI: the built library loads and exports every symbol include/maskahead_hip.h
+declares, the ctypes table matches the header, and argument errors map to the
+reference's exception types -- all without launching a kernel (no GPU needed)."""
+
+import re
+from pathlib import Path
+
+import pytest
+
+from maskahead_amd import _native as N
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "maskahead_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ma_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not N.LIB_PATH.exists():
+        from maskahead_amd.build import build
+
+        build()
+    return N.load()
+
+
+def test_header_declares_the_path():
+    names = _declared()
+    for required in ("ma_dequant_prefix", "ma_splitk_attention", "ma_prefix_scores", "ma_topk_select",
+                     "ma_gather_kv", "ma_quantize_keys", "ma_quantize_values"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_ctypes_table_matches_header():
+    assert sorted(N.SIGNATURES) == _declared()
+
+
+def test_version_and_error_mapping(lib):
+    assert lib.ma_version() >= 1
+    # k > n: rejected on the host before any launch
+    rc = lib.ma_topk_select(1, 8, None, 0, 1, 8, 9, 1, 9, None, None)
+    assert rc == N.MA_EINVAL
+    assert b"bad arguments" in lib.ma_last_error()
+    with pytest.raises(ValueError):
+        N.check(rc, "ma_topk_select")
+    with pytest.raises(N.KernelUnavailableError):
+        N.check(N.MA_EUNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        N.check(N.MA_EHIP, "x")
+
+
+def test_unsupported_prefix_is_reported(lib):
+    p = N.MaPrefix()
+    p.nq, p.kbits, p.vbits, p.kgroup, p.vgroup = 32, 2, 2, 32, 32
+    rc = lib.ma_gather_kv(p, 1, 1, 128, 1, N.i64arr(0, 0), 1, N.MaTensor4(), N.MaTensor4(), None)
+    assert rc == N.MA_EUNSUPPORTED
+    assert b"bit widths" in lib.ma_last_error()
+    rc = lib.ma_splitk_attention(N.MaTensor4(), 1, 28, 32, 96, p, 4, N.MaTensor4(), N.MaTensor4(), 0, 0, 0, 0,
+                                 1.0, N.MaTensor4(), None, None, None, 0, None, 0, None)
+    assert rc == N.MA_EUNSUPPORTED          # head_dim 96 is not built
