@@ -60,23 +60,29 @@ def algorithmic(sh):
     return dict(bytes=pass1 + pass2 + scores + gather, flops=flops1 + flops2, pass1_bytes=pass1, pass1_flops=flops1)
 
 
-def time_graph(fn, steps, warmup, stream):
-    """Capture fn() in a HIP graph; replay `warmup` times untimed, then `steps` times
-    between events on the capture stream.  Returns ms per replay."""
+def time_graph(fn, steps, warmup):
+    """Capture fn() in a HIP graph, then replay it `warmup` times untimed and `steps`
+    times between two events, all on the current stream (the replay stream).  Every
+    kernel launched by fn uses torch's current stream, which is the capture stream
+    during capture.  Returns ms per replay."""
+    side = torch.cuda.Stream()                 # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                                   # allocate / load the kernels outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        fn()                                   # allocate / warm the kernels outside capture
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g, stream=stream):
-            fn()
+    with torch.cuda.graph(g):
+        fn()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
+    e0.record(cur)
     for _ in range(steps):
         g.replay()
-    e1.record(stream)
+    e1.record(cur)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps, g
 
@@ -148,8 +154,7 @@ def main():
         gather_packed_kv(view, idx, out_key=compact_k[:, :, :sh.read_k], out_value=compact_v[:, :, :sh.read_k])
         result["out"], result["idx"] = out, idx
 
-    stream = torch.cuda.Stream(device=dev)      # default priority
-    ms_step, _ = time_graph(step, a.steps, a.warmup, stream)
+    ms_step, _ = time_graph(step, a.steps, a.warmup)
 
     # the dominant kernel alone: split-K pass 1 (same arguments, its own graph)
     lib = N.load()
@@ -161,10 +166,10 @@ def main():
 
     def partial():
         N.check(lib.ma_splitk_partial(qt, sh.b, hq, t, d, pre_native, hkv, kct, vct, t, 0, 0, 0, d ** -0.5,
-                                      a.split_tokens, ws.data_ptr(), ws_bytes, stream.cuda_stream),
-                "ma_splitk_partial")
+                                      a.split_tokens, ws.data_ptr(), ws_bytes,
+                                      torch.cuda.current_stream().cuda_stream), "ma_splitk_partial")
 
-    ms_partial, _ = time_graph(partial, a.steps, a.warmup, stream)
+    ms_partial, _ = time_graph(partial, a.steps, a.warmup)
 
     def scores_only():
         _, stats = result["stats_holder"]
@@ -172,7 +177,7 @@ def main():
 
     out0, stats0 = splitk_attention(qg, prefix, kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
     result["stats_holder"] = (out0, stats0)
-    ms_scores, _ = time_graph(scores_only, a.steps, a.warmup, stream)
+    ms_scores, _ = time_graph(scores_only, a.steps, a.warmup)
 
     ms_eager = None
     if a.eager:

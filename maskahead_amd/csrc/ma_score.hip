@@ -9,13 +9,16 @@
 // token and 16 rows: the sum over rows is in-register plus one cross-half exchange, then
 // one LDS reduction over waves.  The value distance reads V once per entry, dequantized
 // (and rounded to bf16 when the reference would read its unpacked bf16 prefix).
+#include <type_traits>
+
 #include "ma_tile.h"
 
 using namespace ma;
 
 namespace {
 
-constexpr int MAX_WAVES = 8;
+constexpr int MAX_WAVES = NT / 64;
+enum { SRC_PACKED = 0, SRC_DENSE = 1 };
 
 struct ScoreArgs {
     ma_tensor4 q;
@@ -27,79 +30,202 @@ struct ScoreArgs {
     float sl2;
 };
 
-template <int D, int RPW>
-__global__ void __launch_bounds__(MAX_WAVES * 64) score_kernel(ScoreArgs a) {
-    __shared__ TileLds<D> L;
+// distance partials of a packed V item: tokens 2tp, 2tp+1, channels cg*32 + ch*16 + 0..15
+template <int D>
+__device__ __forceinline__ void dist_packed(float (*dpart)[D / 16], const PfPacked &pf, const float *cen, int u,
+                                            bool vround) {
+    const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
+    const float s0 = ma_f16_to_f32(pf.w[4] & 0xffff), s1 = ma_f16_to_f32(pf.w[4] >> 16);
+    const float z0 = ma_f16_to_f32(pf.w[5] & 0xffff), z1 = ma_f16_to_f32(pf.w[5] >> 16);
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        float x0 = ma_dq((pf.w[c >> 3] >> ((c & 7) * 4)) & 15u, s0, z0);
+        float x1 = ma_dq((pf.w[2 + (c >> 3)] >> ((c & 7) * 4)) & 15u, s1, z1);
+        if (vround) {
+            x0 = ma_round_bf16(x0);
+            x1 = ma_round_bf16(x1);
+        }
+        const float cc = cen[cg * VGRP + ch * 16 + c];
+        a0 = __builtin_fmaf(x0 - cc, x0 - cc, a0);
+        a1 = __builtin_fmaf(x1 - cc, x1 - cc, a1);
+    }
+    dpart[2 * tp][cg * 2 + ch] = a0;
+    dpart[2 * tp + 1][cg * 2 + ch] = a1;
+}
+
+// distance partials of a 16-bit V item: tokens 2tp, 2tp+1, channels chk*8 + 0..7
+// (the loader already rounded them to bf16, which is what a 16-bit prefix holds)
+template <int D>
+__device__ __forceinline__ void dist_dense(float (*dpart)[D / 16], const PfDense &pf, const float *cen, int tid) {
+    const int tp = tid % (TILE / 2), chk = tid / (TILE / 2);
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x0 = ma_bf16_to_f32((pf.w[8 + (e >> 1)] >> ((e & 1) * 16)) & 0xffffu);
+        const float x1 = ma_bf16_to_f32((pf.w[12 + (e >> 1)] >> ((e & 1) * 16)) & 0xffffu);
+        const float cc = cen[chk * 8 + e];
+        a0 = __builtin_fmaf(x0 - cc, x0 - cc, a0);
+        a1 = __builtin_fmaf(x1 - cc, x1 - cc, a1);
+    }
+    // D/8 chunks fold pairwise into D/16 partial slots
+    atomicAdd(&dpart[2 * tp][chk >> 1], a0);
+    atomicAdd(&dpart[2 * tp + 1][chk >> 1], a1);
+}
+
+// Workgroup = `tiles_per_wg` consecutive 64-token tiles of one (batch, KV head) lane;
+// NT threads.  Tiles of the source kind SRC go through the register prefetch; the tile
+// straddling a packed prefix's 16-bit tail is staged synchronously.  The V items of the
+// prefetch feed the value distance directly (no V tile in LDS).
+template <int D, int RPW, int SRC>
+__global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
+    __shared__ TileLds<D> T;
     __shared__ float red[MAX_WAVES][TILE];
     __shared__ float cen[D];
-    __shared__ float dpart[TILE][D / VGRP];
+    __shared__ float dpart[TILE][D / 16];
     constexpr int KS = TileLds<D>::KS;
     constexpr int NKS = D / 16;
-    constexpr int NCG = D / VGRP;
+    constexpr int NDP = D / 16;
 
     const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-    const int tid = threadIdx.x, nthreads = blockDim.x, nwaves = nthreads >> 6;
+    const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
-    const int ntot = a.pre.nq + a.pre.nf;
+    const bool value = a.value, vround = a.vround;
+    const float sl2 = a.sl2;
 
-    if (a.value)
-        for (int d = tid; d < D; d += nthreads) cen[d] = a.centre[(int64_t)bh * D + d];
+    if (value)
+        for (int d = tid; d < D; d += NT) cen[d] = a.centre[(int64_t)bh * D + d];
+    for (int it = tid; it < MAX_WAVES * TILE; it += NT) red[it / TILE][it % TILE] = 0.f;
 
-    // Q fragments (A operand) and per-row softmax statistics of this wave's row tiles
+    // Q fragments (A operand) and per-row statistics of this wave's row tiles
     bf16x8_t qf[RPW][NKS];
     float ml2[RPW][16], il[RPW][16];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-        const int rt = wave + r * nwaves;
+        // all loads from clamped, valid indices and issued unconditionally; padding rows
+        // then select zeros (they contribute exp2(s*0 - 0) * 0 = 0)
+        const int rt = wave + r * MAX_WAVES;
         const int rr = rt * 32 + c32;
         const bool ok = rt < a.row_tiles && rr < a.R2;
-        const int g = ok ? rr / a.T2 : 0;
-        const int t = ok ? min(max(a.q_rows[rr % a.T2], 0), a.T - 1) : 0;  // rows outside the block are clamped
+        const int rrc = ok ? rr : 0;
+        const int g = rrc / a.T2;
+        const int t = min(max(a.q_rows[rrc % a.T2], 0), a.T - 1);  // rows outside the block are clamped
         const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-            qf[r][ks] = ok ? ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype) : bf16x8_t{};
+        for (int ks = 0; ks < NKS; ++ks) qf[r][ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[r][ks] = ok ? qf[r][ks] : bf16x8_t{};
+        int qr[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int ri = rt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
-            float m = 0.f, inv = 0.f;  // padding rows contribute exp2(s*0 - 0) * 0 = 0
-            if (rt < a.row_tiles && ri < a.R2) {
-                const int rf = (ri / a.T2) * a.T + min(max(a.q_rows[ri % a.T2], 0), a.T - 1);
-                const float mpv = a.mp[(int64_t)bh * a.R + rf], lpv = a.lp[(int64_t)bh * a.R + rf];
-                m = mpv * MA_LOG2E;
-                inv = 1.0f / (lpv > 0.f ? lpv : 1.0f);
-            }
-            ml2[r][i] = m;
-            il[r][i] = inv;
+            qr[i] = a.q_rows[(ri < a.R2 ? ri : 0) % a.T2];
+        }
+        float mpv[16], lpv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int ri = rt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
+            const int ric = ri < a.R2 ? ri : 0;
+            const int rf = (ric / a.T2) * a.T + min(max(qr[i], 0), a.T - 1);
+            mpv[i] = a.mp[(int64_t)bh * a.R + rf];
+            lpv[i] = a.lp[(int64_t)bh * a.R + rf];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int ri = rt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
+            const bool rok = rt < a.row_tiles && ri < a.R2;
+            ml2[r][i] = rok ? mpv[i] * MA_LOG2E : 0.f;
+            il[r][i] = rok ? 1.0f / (lpv[i] > 0.f ? lpv[i] : 1.0f) : 0.f;
         }
     }
     const float inv_r2 = 1.0f / (float)a.R2;
+    const int row_tiles = a.row_tiles;
+    float *mass_out = a.mass + (int64_t)bh * (a.pre.nq + a.pre.nf);
+    float *score_out = a.score ? a.score + (int64_t)bh * (a.pre.nq + a.pre.nf) : nullptr;
 
+    const Lane L = make_lane(a.pre, b, h, bh);
+    const int nq = L.nq, ntot = L.ntot;
+    const ItemOffsets off = SRC == SRC_PACKED ? packed_offsets<D>(L, tid) : dense_offsets<D>(L.kf_n, L.vf_n, L.esz, tid);
     const int tile0 = blockIdx.x * a.tiles_per_wg;
-    for (int tt = 0; tt < a.tiles_per_wg; ++tt) {
-        const int n0 = (tile0 + tt) * TILE;
-        if (n0 >= ntot) break;
+    const int ntiles = min(a.tiles_per_wg, (ntot + TILE - 1) / TILE - tile0);
+    using PF = typename std::conditional<SRC == SRC_PACKED, PfPacked, PfDense>::type;
+    auto prefetched = [&](int i) {
+        return prefix_tile_kind(nq, (tile0 + i) * TILE, ntot) == (SRC == SRC_PACKED ? TK_PACKED : TK_DENSE);
+    };
+    auto load = [&](int i, PF &pf) {
+        const int n0 = (tile0 + i) * TILE;
+        if constexpr (SRC == SRC_PACKED) {
+            load_packed<D, true>(pf, L, off, n0, ntot, tid);
+        } else {
+            const int64_t tb = (int64_t)(n0 - nq);
+            load_dense<D, true>(pf, L.kf + tb * L.kf_n * L.esz, L.vf + tb * L.vf_n * L.esz, L.kf_n, L.vf_n, L.fdtype,
+                                L.esz, off, &L, n0, ntot, tid);
+        }
+    };
+    // an f32 prefix keeps f32 values for the distance (splitk.py:364-369 reads them as
+    // stored); the 16-bit loader rounds to bf16, so such tiles take the exact path
+    const bool exact_v = SRC == SRC_DENSE && L.fdtype == MA_F32;
+    auto dist_generic = [&](int n0) {
+        for (int it = tid; it < TILE * NDP; it += NT) {
+            const int tl = it / NDP, c0 = (it % NDP) * 16;
+            const int j = n0 + tl;
+            float ss = 0.f;
+            if (j < ntot) {
+                for (int c = 0; c < 16; ++c) {
+                    float x = lane_value(L, j, c0 + c);
+                    if (vround) x = ma_round_bf16(x);
+                    const float dl = x - cen[c0 + c];
+                    ss = __builtin_fmaf(dl, dl, ss);
+                }
+            }
+            dpart[tl][it % NDP] = ss;
+        }
+    };
+
+    PF pf;
+    if (ntiles > 0 && prefetched(0)) load(0, pf);
+    for (int i = 0; i < ntiles; ++i) {
+        const int n0 = (tile0 + i) * TILE;
+        const bool pre_i = prefetched(i);
         __syncthreads();
-        stage_prefix_tile<D, false>(L, a.pre, b, h, bh, n0, ntot, tid, nthreads);
+        if (pre_i) {
+            if constexpr (SRC == SRC_PACKED) {
+                store_packed<D, false>(T, pf, tid);
+                if (value && tid >= 2 * D && tid < 4 * D) dist_packed<D>(dpart, pf, cen, tid - 2 * D, vround);
+            } else {
+                if (value && !exact_v)
+                    for (int it = tid; it < TILE * NDP; it += NT) dpart[it / NDP][it % NDP] = 0.f;
+                store_dense<D, false>(T, pf, tid);
+            }
+            store_okmask(T.okmask, pf, tid);
+        } else {
+            stage_generic<D, false>(T, L, n0, ntot, tid);
+        }
+        if (value && (!pre_i || exact_v)) dist_generic(n0);
         __syncthreads();
+        if constexpr (SRC == SRC_DENSE) {
+            // 16-bit V items fold into the zeroed partial slots after the barrier
+            if (value && !exact_v && pre_i && tid < TILE / 2 * D / 8) dist_dense<D>(dpart, pf, cen, tid);
+        }
+        if (i + 1 < ntiles && prefetched(i + 1)) load(i + 1, pf);
 
         float part[2] = {0.f, 0.f};  // this lane's token in each 32-token sub-tile
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-            if (wave + r * nwaves >= a.row_tiles) break;
+            if (wave + r * MAX_WAVES >= row_tiles) break;
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                f32x16_t s = f32x16_t{};
+            for (int t2 = 0; t2 < 2; ++t2) {
+                f32x16_t sv = f32x16_t{};
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    bf16x8_t kb = *(const bf16x8_t *)&L.k[(st * 32 + c32) * KS + ks * 16 + hf * 8];
-                    s = ma_mfma32(qf[r][ks], kb, s);
+                    const bf16x8_t kb = *(const bf16x8_t *)&T.k[(t2 * 32 + c32) * KS + ks * 16 + hf * 8];
+                    sv = ma_mfma32(qf[r][ks], kb, sv);
                 }
                 float acc = 0.f;
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    acc += exp2f(__builtin_fmaf(s[i], a.sl2, -ml2[r][i])) * il[r][i];
-                part[st] += acc;
+                for (int e = 0; e < 16; ++e)
+                    acc = __builtin_fmaf(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], sl2, -ml2[r][e])), il[r][e], acc);
+                part[t2] += acc;
             }
         }
         part[0] = ma_sum_xor32(part[0]);
@@ -109,72 +235,61 @@ __global__ void __launch_bounds__(MAX_WAVES * 64) score_kernel(ScoreArgs a) {
             red[wave][32 + c32] = part[1];
         }
         __syncthreads();
-        // one thread per token: sum over waves, mask, store mass; keep it for the score
-        float mass_j = 0.f;
-        const int j = n0 + tid;
-        const bool live = tid < TILE && j < ntot && ((L.okmask >> tid) & 1);
-        if (tid < TILE && j < ntot) {
-            float s = 0.f;
-            for (int w = 0; w < nwaves; ++w) s += red[w][tid];
-            mass_j = live ? s * inv_r2 : 0.f;
-            a.mass[(int64_t)bh * ntot + j] = mass_j;
-        }
-        if (!a.value) continue;
-        // value distance: item = (token, channel group)
-        for (int it = tid; it < TILE * NCG; it += nthreads) {
-            const int tl = it / NCG, cg = it % NCG;
-            const int jj = n0 + tl;
-            float ss = 0.f;
-            if (jj < ntot) {
-                if (jj < a.pre.nq) {
-                    const uint8_t *src = a.pre.vq + b * a.pre.svq[0] + h * a.pre.svq[1] + (int64_t)jj * a.pre.svq[2] +
-                                         (int64_t)cg * a.pre.svq[3];
-                    const uint4 w = *(const uint4 *)src;
-                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-                    const int64_t so = b * a.pre.svs[0] + h * a.pre.svs[1] + (int64_t)jj * a.pre.svs[2] + cg;
-                    const float sc = ma_f16_to_f32(a.pre.vs[so]), zp = ma_f16_to_f32(a.pre.vz[so]);
+        if (tid < TILE) {
+            const int j = n0 + tid;
+            if (j < ntot) {
+                const bool live = (T.okmask >> tid) & 1;
+                float sm = 0.f;
 #pragma unroll
-                    for (int c = 0; c < VGRP; ++c) {
-                        float x = ma_dq((wv[c >> 3] >> ((c & 7) * 4)) & 15u, sc, zp);
-                        if (a.vround) x = ma_round_bf16(x);
-                        const float dlt = x - cen[cg * VGRP + c];
-                        ss = __builtin_fmaf(dlt, dlt, ss);
-                    }
-                } else {
-                    const int64_t vb = b * a.pre.svf[0] + h * a.pre.svf[1] + (int64_t)(jj - a.pre.nq) * a.pre.svf[2] +
-                                       cg * VGRP;
+                for (int w = 0; w < MAX_WAVES; ++w) sm += red[w][tid];
+                const float mass_j = live ? sm * inv_r2 : 0.f;
+                mass_out[j] = mass_j;
+                if (value) {
+                    float ss = 0.f;
 #pragma unroll
-                    for (int c = 0; c < VGRP; ++c) {
-                        float x = ma_load_f(a.pre.vf, vb + c, a.pre.fdtype);
-                        if (a.vround) x = ma_round_bf16(x);
-                        const float dlt = x - cen[cg * VGRP + c];
-                        ss = __builtin_fmaf(dlt, dlt, ss);
-                    }
+                    for (int c = 0; c < NDP; ++c) ss += dpart[tid][c];
+                    score_out[j] = live ? mass_j * sqrtf(ss) : 0.f;
                 }
             }
-            dpart[tl][cg] = ss;
-        }
-        __syncthreads();
-        if (tid < TILE && j < ntot) {
-            float ss = 0.f;
-#pragma unroll
-            for (int cg = 0; cg < NCG; ++cg) ss += dpart[tid][cg];
-            a.score[(int64_t)bh * ntot + j] = live ? mass_j * sqrtf(ss) : 0.f;
         }
     }
 }
 
-// centre[b,h,:] = mean over rows g*T + q_rows[t2] of f32(op); grid B*H, D threads.
-__global__ void centre_kernel(const void *op, int op_dtype, int G, int T, int D, const int32_t *q_rows, int T2,
-                              float *centre) {
-    const int bh = blockIdx.x, d = threadIdx.x;
-    if (d >= D) return;
-    const int R = G * T;
+// centre[b,h,:] = mean over rows g*T + q_rows[t2] of f32(op); grid B*H, 1024 threads:
+// D channels x (1024/D) row slices summed in a fixed order, so the result is
+// deterministic.
+__global__ void __launch_bounds__(1024) centre_kernel(const void *op, int op_dtype, int G, int T, int D,
+                                                      const int32_t *q_rows, int T2, float *centre) {
+    __shared__ float part[1024];
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const int slices = 1024 / D, d = tid % D, sl = tid / D;
+    const int R = G * T, R2 = G * T2;
     float s = 0.f;
-    for (int g = 0; g < G; ++g)
-        for (int t2 = 0; t2 < T2; ++t2)
-            s += ma_load_f(op, ((int64_t)bh * R + g * T + min(max(q_rows[t2], 0), T - 1)) * D + d, op_dtype);
-    centre[(int64_t)bh * D + d] = s / (float)(G * T2);
+    // one loop per dtype: no branch around the loads, which can then all be in flight
+    if (op_dtype == MA_F32) {
+        const float *o = (const float *)op;
+#pragma unroll 8
+        for (int rr = sl; rr < R2; rr += slices) {
+            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
+            s += o[((int64_t)bh * R + row) * D + d];
+        }
+    } else {
+        const uint16_t *o = (const uint16_t *)op;
+        const bool bf = op_dtype == MA_BF16;
+#pragma unroll 8
+        for (int rr = sl; rr < R2; rr += slices) {
+            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
+            const uint16_t x = o[((int64_t)bh * R + row) * D + d];
+            s += bf ? ma_bf16_to_f32(x) : ma_f16_to_f32(x);
+        }
+    }
+    part[tid] = s;
+    __syncthreads();
+    if (sl == 0) {
+        float t = 0.f;
+        for (int k = 0; k < slices; ++k) t += part[k * D + d];
+        centre[(int64_t)bh * D + d] = t / (float)R2;
+    }
 }
 
 }  // namespace
@@ -183,12 +298,12 @@ int ma_validate_prefix(const ma_prefix *p, int D, const char *who);
 
 extern "C" int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, int D, const int32_t *q_rows,
                                int T2, float *centre, void *stream) {
-    if (!op || !q_rows || !centre || B <= 0 || H <= 0 || G <= 0 || T <= 0 || T2 <= 0 || D <= 0 || D > 1024) {
+    if (!op || !q_rows || !centre || B <= 0 || H <= 0 || G <= 0 || T <= 0 || T2 <= 0 || (D != 64 && D != 128)) {
         ma_set_error("ma_value_centre: bad arguments");
         return MA_EINVAL;
     }
-    hipLaunchKernelGGL(centre_kernel, dim3(B * H), dim3(D), 0, (hipStream_t)stream, op, op_dtype, G, T, D, q_rows, T2,
-                       centre);
+    hipLaunchKernelGGL(centre_kernel, dim3(B * H), dim3(1024), 0, (hipStream_t)stream, op, op_dtype, G, T, D, q_rows,
+                       T2, centre);
     return ma_check_launch("ma_value_centre");
 }
 
@@ -216,8 +331,7 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     }
     const int n = p->nq + p->nf;
     if (n == 0) return MA_OK;
-    const int waves = row_tiles < MAX_WAVES ? row_tiles : MAX_WAVES;
-    const int rpw = (row_tiles + waves - 1) / waves;
+    const int rpw = (row_tiles + MAX_WAVES - 1) / MAX_WAVES;
     const int tiles = (n + TILE - 1) / TILE;
     int per = (tiles * B * H + ma_num_cus() - 1) / ma_num_cus();
     if (per < 1) per = 1;
@@ -242,14 +356,17 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     sa.vround = v_round_bf16;
     sa.sl2 = scale * MA_LOG2E;
     dim3 grid((tiles + per - 1) / per, B * H);
-    dim3 block(waves * 64);
+    dim3 block(NT);
     hipStream_t st = (hipStream_t)stream;
+    const bool packed = p->nq > 0;
+#define MA_SCORE(D_, R_, S_) hipLaunchKernelGGL((score_kernel<D_, R_, S_>), grid, block, 0, st, sa)
     if (D == 128) {
-        if (rpw == 1) hipLaunchKernelGGL((score_kernel<128, 1>), grid, block, 0, st, sa);
-        else hipLaunchKernelGGL((score_kernel<128, 2>), grid, block, 0, st, sa);
+        if (rpw == 1) { if (packed) MA_SCORE(128, 1, SRC_PACKED); else MA_SCORE(128, 1, SRC_DENSE); }
+        else { if (packed) MA_SCORE(128, 2, SRC_PACKED); else MA_SCORE(128, 2, SRC_DENSE); }
     } else {
-        if (rpw == 1) hipLaunchKernelGGL((score_kernel<64, 1>), grid, block, 0, st, sa);
-        else hipLaunchKernelGGL((score_kernel<64, 2>), grid, block, 0, st, sa);
+        if (rpw == 1) { if (packed) MA_SCORE(64, 1, SRC_PACKED); else MA_SCORE(64, 1, SRC_DENSE); }
+        else { if (packed) MA_SCORE(64, 2, SRC_PACKED); else MA_SCORE(64, 2, SRC_DENSE); }
     }
+#undef MA_SCORE
     return ma_check_launch(who);
 }

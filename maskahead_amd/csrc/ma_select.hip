@@ -16,99 +16,132 @@ namespace {
 constexpr int NT = 1024;
 constexpr int NW = NT / 64;
 
-__device__ __forceinline__ int block_sum(int v, int *sh) {
-    v = ma_wave_sum_i(v);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
-    if (lane == 0) sh[wave] = v;
-    __syncthreads();
-    int s = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) s += sh[w];
-    return s;
-}
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-// exclusive prefix sum over threads in index order; *total gets the block total
-__device__ __forceinline__ int block_exclusive_scan(int v, int *sh, int *total) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-    }
-    __syncthreads();
-    if (lane == 63) sh[wave] = incl;
-    __syncthreads();
-    int before = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        const int x = sh[w];
-        if (w < wave) before += x;
-        all += x;
-    }
-    *total = all;
-    return before + incl - v;
-}
-
+// One workgroup per row.  Element j = e*NT + tid belongs to thread tid (slot e), so every
+// load is coalesced and, within a slot, index order is thread order.  Counting uses wave
+// ballots (a popcount per wave, no shuffles); the k-th largest key T is found by a
+// most-significant-bit-first bisection, one barrier per bit (double-buffered counts).
+// Output slot of a selected element = selected elements in earlier slots + in earlier
+// waves of its slot + lanes below it in its wave: ascending indices, no sort.
 template <int VPT>
 __global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t rank_stride, const uint8_t *mask,
                                                   int64_t mask_stride, int n, int k, int64_t *idx,
                                                   int64_t idx_stride, float *values) {
-    __shared__ int sh[NW];
-    const int row = blockIdx.x, tid = threadIdx.x;
+    __shared__ int cnt2[2][NW];
+    __shared__ int c_gt[VPT][NW], c_eq[VPT][NW], c_sel[VPT][NW];
+    __shared__ int p_eq[VPT + 1], p_sel[VPT + 1];
+    static_assert(VPT <= 64, "one wave scans the slots");
+    const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
     const float *rr = rank + (int64_t)row * rank_stride;
     const uint8_t *mr = mask ? mask + (int64_t)row * mask_stride : nullptr;
-    const int base = tid * VPT;
     uint32_t key[VPT];
+    // branchless loads from clamped indices, so all VPT loads are in flight at once
+    float v[VPT];
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) v[e] = rr[min(e * NT + tid, n - 1)];
+    uint32_t live = 0xffffffffu;
+    if (mr) {
+        uint8_t mb[VPT];
+#pragma unroll
+        for (int e = 0; e < VPT; ++e) mb[e] = mr[min(e * NT + tid, n - 1)];
+#pragma unroll
+        for (int e = 0; e < VPT; ++e) v[e] = mb[e] ? v[e] : -INFINITY;
+    }
+    (void)live;
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-        const int j = base + e;
-        uint32_t kk = 0u;  // below every real key (-inf maps to 0x007fffff)
-        if (j < n) kk = ma_order_key((mr && !mr[j]) ? -INFINITY : rr[j]);
-        key[e] = kk;
+        const int j = e * NT + tid;
+        key[e] = j < n ? ma_order_key(v[e]) : 0u;  // 0: below every real key (-inf maps to 0x007fffff)
     }
     uint32_t thr = 0u;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = thr | (1u << bit);
         int c = 0;
 #pragma unroll
-        for (int e = 0; e < VPT; ++e) c += key[e] >= cand;
-        if (block_sum(c, sh) >= k) thr = cand;
+        for (int e = 0; e < VPT; ++e) c += __popcll(__ballot(key[e] >= cand));
+        if (lane == 0) cnt2[bit & 1][wave] = c;
+        __syncthreads();
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot += cnt2[bit & 1][w];
+        if (tot >= k) thr = cand;
     }
-    int gt = 0, eq = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-        gt += key[e] > thr;
-        eq += key[e] == thr;
+        const uint64_t bg = __ballot(key[e] > thr);
+        const uint64_t be = __ballot(key[e] == thr);
+        if (lane == 0) {
+            c_gt[e][wave] = __popcll(bg);
+            c_eq[e][wave] = __popcll(be);
+        }
     }
-    const int n_gt = block_sum(gt, sh);
-    int eq_total;
-    const int eq_start = block_exclusive_scan(eq, sh, &eq_total);
-    const int need = k - n_gt;
-    int nsel = 0, eq_before = eq_start;
+    __syncthreads();
+    // wave 0, lane e: slot e's counts -> exclusive prefix over waves (in place) and, by a
+    // wave scan, over slots; the gt total gives the number of equal keys still needed
+    if (wave == 0) {
+        int eq_tot = 0, gt_tot = 0;
+        if (lane < VPT) {
+            for (int w = 0; w < NW; ++w) {
+                const int c = c_eq[lane][w];
+                c_eq[lane][w] = eq_tot;
+                eq_tot += c;
+                gt_tot += c_gt[lane][w];
+            }
+        }
+        int incl = eq_tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        gt_tot = ma_wave_sum_i(gt_tot);
+        if (lane < VPT) p_eq[lane] = incl - eq_tot;
+        if (lane == 0) p_eq[VPT] = k - gt_tot;  // equal keys still needed
+    }
+    __syncthreads();
+    const int need = p_eq[VPT];
+    uint64_t selbits = 0;  // bit e: this thread's slot-e element is selected
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
         const bool is_eq = key[e] == thr;
-        nsel += (key[e] > thr) || (is_eq && eq_before < need);
-        eq_before += is_eq;
+        const int eb = p_eq[e] + c_eq[e][wave] + __popcll(__ballot(is_eq) & below);
+        const bool sl = key[e] > thr || (is_eq && eb < need);
+        selbits |= (uint64_t)sl << e;
+        const uint64_t bs = __ballot(sl);
+        if (lane == 0) c_sel[e][wave] = __popcll(bs);
     }
-    int sel_total;
-    int slot = block_exclusive_scan(nsel, sh, &sel_total);
-    // second walk: same decisions, now writing
-    eq_before = eq_start;
+    __syncthreads();
+    if (wave == 0) {
+        int tot = 0;
+        if (lane < VPT) {
+            for (int w = 0; w < NW; ++w) {
+                const int c = c_sel[lane][w];
+                c_sel[lane][w] = tot;
+                tot += c;
+            }
+        }
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        if (lane < VPT) p_sel[lane] = incl - tot;
+    }
+    __syncthreads();
     int64_t *out = idx + (int64_t)row * idx_stride;
     float *vout = values ? values + (int64_t)row * k : nullptr;
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-        const bool is_eq = key[e] == thr;
-        const bool sel = (key[e] > thr) || (is_eq && eq_before < need);
-        eq_before += is_eq;
-        if (sel && slot < k) {
-            const int j = base + e;
+        const bool sl = (selbits >> e) & 1;
+        const uint64_t bs = __ballot(sl);
+        const int slot = p_sel[e] + c_sel[e][wave] + __popcll(bs & below);
+        if (sl && slot < k) {
+            const int j = e * NT + tid;
             out[slot] = j;
-            if (vout) vout[slot] = (mr && !mr[j]) ? -INFINITY : rr[j];
-            ++slot;
+            if (vout) vout[slot] = v[e];
         }
     }
 }

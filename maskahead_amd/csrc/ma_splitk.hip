@@ -13,13 +13,18 @@
 // O^T accumulator keeps the lane's row too, so the online-softmax rescale is per lane.
 // Pass 2 (splitk_combine_kernel): log-sum-exp merge of the partials into the output and
 // the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
+#include <type_traits>
+
 #include "ma_tile.h"
 
 using namespace ma;
 
 namespace {
 
-constexpr int MAX_WAVES = 8;
+constexpr int MAX_WAVES = NT / 64;
+// a row's running reference max is raised only when a tile's max exceeds it by more than
+// 2^8 in exp2 units, so most tiles skip the accumulator rescale; p <= 2^8 stays exact
+constexpr float LAZY_LOG2 = 8.0f;
 
 struct FwdArgs {
     ma_tensor4 q;
@@ -31,16 +36,136 @@ struct FwdArgs {
     float *wm, *wl, *wacc;  // partials [B*H][nsplit+1][R] and [..][R][D]
 };
 
+// Online-softmax state of one query row (the lane's column of S^T); l and acc are
+// relative to m_ref, m_true is the exact running max (raw logit units).
 template <int D>
-__global__ void __launch_bounds__(MAX_WAVES * 64) splitk_fwd_kernel(FwdArgs a) {
-    __shared__ TileLds<D> L;
+struct RowState {
+    float m_ref, m_true, l;
+    f32x16_t acc[D / 32];
+};
+
+template <int D>
+__device__ __forceinline__ void row_reset(RowState<D> &st) {
+    st.m_ref = -INFINITY;
+    st.m_true = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) st.acc[dt] = f32x16_t{};
+}
+
+// One 64-token tile for a wave's 32 rows: S^T = K Q^T, online softmax, O^T += V^T P^T.
+template <int D>
+__device__ __forceinline__ void attend_tile(const TileLds<D> &L, const bf16x8_t *qf, RowState<D> &st, int c32, int hf,
+                                            bool need_mask, int lim, float sl2) {
     constexpr int KS = TileLds<D>::KS, VS = TileLds<D>::VS;
-    constexpr int NKS = D / 16;  // MFMA k-steps over the head dim
-    constexpr int NDT = D / 32;  // 32-channel tiles of the accumulator
+    constexpr int NKS = D / 16, NDT = D / 32;
+    f32x16_t s[2];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+        s[t2] = f32x16_t{};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const bf16x8_t ka = *(const bf16x8_t *)&L.k[(t2 * 32 + c32) * KS + ks * 16 + hf * 8];
+            s[t2] = ma_mfma32(ka, qf[ks], s[t2]);
+        }
+    }
+    // element i of s[t2] <-> token t2*32 + (i/4)*8 + hf*4 + i%4
+    if (need_mask) {
+        const uint64_t okm = L.okmask >> (hf * 4);
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int tk = t2 * 32 + (i >> 2) * 8 + (i & 3);
+                const bool ok = ((okm >> tk) & 1) && tk < lim;
+                s[t2][i] = ok ? s[t2][i] : -INFINITY;
+            }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[t2][i]);
+    mt = ma_max_xor32(mt);
+    st.m_true = fmaxf(st.m_true, mt);
+    const bool need = (mt - st.m_ref) * sl2 > LAZY_LOG2;   // false for NaN (both -inf)
+    if (__any(need)) {
+        const float m_new = need ? mt : st.m_ref;
+        const float alpha = (m_new == st.m_ref) ? 1.0f : __builtin_amdgcn_exp2f((st.m_ref - m_new) * sl2);
+        st.l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) st.acc[dt] *= alpha;
+        st.m_ref = m_new;
+    }
+    const float off = (st.m_ref == -INFINITY) ? 0.f : -st.m_ref * sl2;
+    float ls = 0.f;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t2][i], sl2, off));
+            s[t2][i] = p;
+            ls += p;
+        }
+    st.l += ma_sum_xor32(ls);
+    // P^T chunks (B operand): chunk c = 16 tokens, lane holds s[c/2][8*(c%2) .. +7]
+    bf16x8_t pb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)s[c >> 1][(c & 1) * 8 + j];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        const uint16_t *vrow = &L.vt[(dt * 32 + c32) * VS];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const bf16x4_t lo = *(const bf16x4_t *)&vrow[c * 16 + hf * 4];
+            const bf16x4_t hi = *(const bf16x4_t *)&vrow[c * 16 + 8 + hf * 4];
+            const bf16x8_t va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            st.acc[dt] = ma_mfma32(va, pb[c], st.acc[dt]);
+        }
+    }
+}
+
+// write a row's partial (max in natural-log units, l and acc relative to the exact max)
+template <int D>
+__device__ __forceinline__ void write_partial(const FwdArgs &a, const RowState<D> &st, int bh, int slot, int row,
+                                              int hf) {
+    constexpr int NDT = D / 32;
+    const int64_t prow = ((int64_t)bh * (a.nsplit + 1) + slot) * a.R + row;
+    float f = 0.f;
+    if (st.m_true != -INFINITY) f = __builtin_amdgcn_exp2f((st.m_ref - st.m_true) * a.sl2);
+    if (hf == 0) {
+        a.wm[prow] = st.m_true * a.scale;
+        a.wl[prow] = st.l * f;
+    }
+    float *dst = a.wacc + prow * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4_t v = {st.acc[dt][q4 * 4 + 0] * f, st.acc[dt][q4 * 4 + 1] * f, st.acc[dt][q4 * 4 + 2] * f,
+                               st.acc[dt][q4 * 4 + 3] * f};
+            *(f32x4_t *)&dst[dt * 32 + q4 * 8 + hf * 4] = v;
+        }
+}
+
+enum { SRC_PACKED = 0, SRC_DENSE = 1 };
+
+// grid (max(nsplit,1), B*H, row groups), NT threads.  Split sp covers prefix tokens
+// [sp*split_n, (sp+1)*split_n); split 0 also attends the current block afterwards and
+// writes it as partial slot nsplit.  The prefix tiles of the source kind SRC run through
+// the register prefetch (the next tile's loads are in flight while the current one is
+// computed); with a packed prefix, its 16-bit residual tail and the current block are
+// staged synchronously (a few tiles per call).
+template <int D, int SRC>
+__global__ void __launch_bounds__(NT) splitk_fwd_kernel(FwdArgs a) {
+    __shared__ TileLds<D> T;
+    constexpr int NKS = D / 16;
 
     const int sp = blockIdx.x, bh = blockIdx.y;
     const int b = bh / a.H, h = bh % a.H;
-    const int tid = threadIdx.x, nthreads = blockDim.x;
+    const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
     const int rtile = blockIdx.z * MAX_WAVES + wave;
     const int row = rtile * 32 + c32;
@@ -48,119 +173,96 @@ __global__ void __launch_bounds__(MAX_WAVES * 64) splitk_fwd_kernel(FwdArgs a) {
     const bool row_ok = row < a.R;
     const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
 
-    // Q^T fragments (B operand): Q[row][ks*16 + hf*8 .. +7], zero for padding rows
     bf16x8_t qf[NKS];
     {
         const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-            qf[ks] = row_ok ? ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype) : bf16x8_t{};
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
     }
 
-    float m_i = -INFINITY, l_i = 0.f;
-    f32x16_t acc[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-
-    const bool is_cur = sp == a.nsplit;
-    const int ntot = a.pre.nq + a.pre.nf;
-    const int start = is_cur ? 0 : sp * a.split_n;
-    const int end = is_cur ? a.Tc : min(start + a.split_n, ntot);
+    const Lane L = make_lane(a.pre, b, h, bh);
+    const Dense kc = dense_lane(a.kc.ptr, a.kc.s, a.kc.dtype, b, h);
+    const Dense vc = dense_lane(a.vc.ptr, a.vc.s, a.vc.dtype, b, h);
+    const int nq = L.nq, ntot = L.ntot, Tc = a.Tc;
+    const int pstart = sp * a.split_n;
+    const int pend = min(pstart + a.split_n, ntot);
+    const int n_pt = pstart < pend ? (pend - pstart + TILE - 1) / TILE : 0;
+    const bool with_cur = sp == 0;
+    const int n_ct = with_cur ? (Tc + TILE - 1) / TILE : 0;
+    const int total = n_pt + n_ct;
     const int qpos = a.q_pos0 + t;
+    const int causal = a.causal, c_pos0 = a.c_pos0;
+    const float sl2 = a.sl2;
 
-    for (int n0 = start; n0 < end; n0 += TILE) {
+    const ItemOffsets off = SRC == SRC_PACKED ? packed_offsets<D>(L, tid) : dense_offsets<D>(L.kf_n, L.vf_n, L.esz, tid);
+    const ItemOffsets coff = dense_offsets<D>(kc.sn, vc.sn, kc.esz, tid);
+
+    auto tile_n0 = [&](int i) { return i < n_pt ? pstart + i * TILE : (i - n_pt) * TILE; };
+    // does tile i go through the prefetch block?
+    auto prefetched = [&](int i) {
+        if (i >= n_pt) return SRC == SRC_DENSE;
+        return prefix_tile_kind(nq, tile_n0(i), pend) == (SRC == SRC_PACKED ? TK_PACKED : TK_DENSE);
+    };
+    using PF = typename std::conditional<SRC == SRC_PACKED, PfPacked, PfDense>::type;
+    auto load = [&](int i, PF &pf) {
+        const int n0 = tile_n0(i);
+        if constexpr (SRC == SRC_PACKED) {
+            load_packed<D, true>(pf, L, off, n0, pend, tid);
+        } else {
+            if (i < n_pt) {
+                const int64_t tb = (int64_t)(n0 - nq);
+                load_dense<D, true>(pf, L.kf + tb * L.kf_n * L.esz, L.vf + tb * L.vf_n * L.esz, L.kf_n, L.vf_n,
+                                    L.fdtype, L.esz, off, &L, n0, pend, tid);
+            } else {
+                load_dense<D, true>(pf, kc.base + (int64_t)n0 * kc.sn * kc.esz, vc.base + (int64_t)n0 * vc.sn * vc.esz,
+                                    kc.sn, vc.sn, kc.dtype, kc.esz, coff, nullptr, n0, Tc, tid);
+            }
+        }
+    };
+
+    RowState<D> st;
+    row_reset(st);
+    PF pf;
+    if (total > 0 && prefetched(0)) load(0, pf);
+    for (int i = 0; i < total; ++i) {
+        const bool cur = i >= n_pt;
+        const int n0 = tile_n0(i);
+        const int end = cur ? Tc : pend;
         __syncthreads();
-        if (is_cur) stage_dense_tile<D>(L, a.kc, a.vc, b, h, n0, end, tid, nthreads);
-        else stage_prefix_tile<D, true>(L, a.pre, b, h, bh, n0, end, tid, nthreads);
+        if (prefetched(i)) {
+            if constexpr (SRC == SRC_PACKED) store_packed<D, true>(T, pf, tid);
+            else store_dense<D, true>(T, pf, tid);
+            store_okmask(T.okmask, pf, tid);
+        } else if (cur) {
+            PfDense tmp;
+            load_dense<D, true>(tmp, kc.base + (int64_t)n0 * kc.sn * kc.esz, vc.base + (int64_t)n0 * vc.sn * vc.esz,
+                                kc.sn, vc.sn, kc.dtype, kc.esz, coff, nullptr, n0, Tc, tid);
+            store_dense<D, true>(T, tmp, tid);
+            store_okmask(T.okmask, tmp, tid);
+        } else {
+            stage_generic<D, true>(T, L, n0, end, tid);
+        }
         __syncthreads();
-        if (!wave_active) continue;
-
-        // S^T for two 32-token sub-tiles: element i <-> token st*32 + (i/4)*8 + hf*4 + i%4
-        f32x16_t s[2];
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            s[st] = f32x16_t{};
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) {
-                bf16x8_t ka = *(const bf16x8_t *)&L.k[(st * 32 + c32) * KS + ks * 16 + hf * 8];
-                s[st] = ma_mfma32(ka, qf[ks], s[st]);
-            }
+        if (i + 1 < total && prefetched(i + 1)) load(i + 1, pf);
+        if (wave_active) {
+            const bool cz = cur && causal > 0;
+            const int lim = cz ? (qpos / causal + 1) * causal - c_pos0 - n0 - hf * 4 : TILE;
+            const bool need_mask = cz || T.okmask != ~0ull;
+            attend_tile<D>(T, qf, st, c32, hf, need_mask, lim, sl2);
         }
-        // usable tokens: tile mask, and for the current block the block-causal limit
-        // (c_pos0+j)/cb <= qpos/cb  <=>  j < (qpos/cb + 1)*cb - c_pos0  (splitk.py:175-176)
-        const uint64_t okm = L.okmask >> (hf * 4);
-        int lim = TILE;
-        if (is_cur && a.causal > 0) lim = (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4;
-        float mt = -INFINITY;
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int tk = st * 32 + (i >> 2) * 8 + (i & 3);  // token minus hf*4
-                const bool ok = ((okm >> tk) & 1) && tk < lim;
-                const float v = ok ? s[st][i] : -INFINITY;
-                s[st][i] = v;
-                mt = fmaxf(mt, v);
-            }
-        }
-        mt = ma_max_xor32(mt);
-        const float m_new = fmaxf(m_i, mt);
-        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = exp2f((m_i - ms) * a.sl2);
-        const float off = -ms * a.sl2;
-        float ls = 0.f;
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = exp2f(__builtin_fmaf(s[st][i], a.sl2, off));
-                s[st][i] = p;
-                ls += p;
-            }
-        }
-        ls = ma_sum_xor32(ls);
-        l_i = l_i * alpha + ls;
-        m_i = m_new;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
-
-        // P^T chunks (B operand): chunk c = 16 tokens, lane holds s[c/2][8*(c%2) .. +7]
-        bf16x8_t pb[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)s[c >> 1][(c & 1) * 8 + j];
-        }
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-            const uint16_t *vrow = &L.vt[(dt * 32 + c32) * VS];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const bf16x4_t lo = *(const bf16x4_t *)&vrow[c * 16 + hf * 4];
-                const bf16x4_t hi = *(const bf16x4_t *)&vrow[c * 16 + 8 + hf * 4];
-                const bf16x8_t va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                acc[dt] = ma_mfma32(va, pb[c], acc[dt]);
-            }
+        if (i == n_pt - 1) {  // prefix segment done
+            if (wave_active && row_ok) write_partial<D>(a, st, bh, sp, row, hf);
+            row_reset(st);
         }
     }
-    if (!wave_active || !row_ok) return;
-    const int64_t prow = ((int64_t)bh * (a.nsplit + 1) + sp) * a.R + row;
-    if (hf == 0) {
-        a.wm[prow] = m_i * a.scale;  // natural-log units, as the reference's M
-        a.wl[prow] = l_i;
-    }
-    float *dst = a.wacc + prow * D;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            f32x4_t v = {acc[dt][q4 * 4 + 0], acc[dt][q4 * 4 + 1], acc[dt][q4 * 4 + 2], acc[dt][q4 * 4 + 3]};
-            *(f32x4_t *)&dst[dt * 32 + q4 * 8 + hf * 4] = v;
-        }
-    }
+    if (with_cur && wave_active && row_ok) write_partial<D>(a, st, bh, a.nsplit, row, hf);
 }
 
-// grid (ceil(R / rows_per_block), B*H), 256 threads; D/4 threads per row, 4 channels each.
+// grid (ceil(R / rows_per_block), B*H), 256 threads; D/4 threads per row, 4 channels
+// each.  First the exact maxima over the splits, then every split's weight is known and
+// the loads of different splits are independent.
 template <int D>
 __global__ void __launch_bounds__(256) splitk_combine_kernel(const float *wm, const float *wl, const float *wacc,
                                                              int H, int G, int T, int R, int nsplit, ma_tensor4 out,
@@ -171,19 +273,19 @@ __global__ void __launch_bounds__(256) splitk_combine_kernel(const float *wm, co
     const int row = blockIdx.x * RPB + threadIdx.x / TPR;
     const int d0 = (threadIdx.x % TPR) * 4;
     if (row >= R) return;
-    float mp = -INFINITY, lp = 0.f;
-    f32x4_t op = {0.f, 0.f, 0.f, 0.f};
     const int64_t base = (int64_t)bh * (nsplit + 1) * R + row;
+    float mp = -INFINITY;
+#pragma unroll 16
+    for (int sp = 0; sp < nsplit; ++sp) mp = fmaxf(mp, wm[base + (int64_t)sp * R]);
+    const float msafe_p = (mp == -INFINITY) ? 0.f : mp;
+    float lp = 0.f;
+    f32x4_t op = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
     for (int sp = 0; sp < nsplit; ++sp) {
         const int64_t pr = base + (int64_t)sp * R;
-        const float ms = wm[pr], lsp = wl[pr];
-        const f32x4_t as = *(const f32x4_t *)&wacc[pr * D + d0];
-        const float mn = fmaxf(mp, ms);
-        const float msafe = (mn == -INFINITY) ? 0.f : mn;
-        const float ea = expf(mp - msafe), eb = expf(ms - msafe);
-        lp = lp * ea + lsp * eb;
-        op = op * ea + as * eb;
-        mp = mn;
+        const float w = expf(wm[pr] - msafe_p);
+        lp += wl[pr] * w;
+        op += *(const f32x4_t *)&wacc[pr * D + d0] * w;
     }
     const int64_t pc = base + (int64_t)nsplit * R;
     const float mc = wm[pc], lc = wl[pc];
@@ -319,11 +421,15 @@ int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int
 }
 
 int launch_partial(const Plan &pl, hipStream_t st) {
-    dim3 grid(pl.fa.nsplit + 1, pl.B * pl.fa.H, pl.row_groups);
-    if (pl.D == 128)
-        hipLaunchKernelGGL(splitk_fwd_kernel<128>, grid, dim3(pl.waves * 64), 0, st, pl.fa);
-    else
-        hipLaunchKernelGGL(splitk_fwd_kernel<64>, grid, dim3(pl.waves * 64), 0, st, pl.fa);
+    dim3 grid(pl.fa.nsplit > 0 ? pl.fa.nsplit : 1, pl.B * pl.fa.H, pl.row_groups);
+    const bool packed = pl.fa.pre.nq > 0;
+    if (pl.D == 128) {
+        if (packed) hipLaunchKernelGGL((splitk_fwd_kernel<128, SRC_PACKED>), grid, dim3(NT), 0, st, pl.fa);
+        else hipLaunchKernelGGL((splitk_fwd_kernel<128, SRC_DENSE>), grid, dim3(NT), 0, st, pl.fa);
+    } else {
+        if (packed) hipLaunchKernelGGL((splitk_fwd_kernel<64, SRC_PACKED>), grid, dim3(NT), 0, st, pl.fa);
+        else hipLaunchKernelGGL((splitk_fwd_kernel<64, SRC_DENSE>), grid, dim3(NT), 0, st, pl.fa);
+    }
     return ma_check_launch("ma_splitk_partial");
 }
 

@@ -37,6 +37,8 @@ def topk_ascending(rank: torch.Tensor, k: int, mask: torch.Tensor | None = None,
             m2 = m2.contiguous()
     if out is None:
         out = torch.empty((*rank.shape[:-1], k), device=rank.device, dtype=torch.int64)
+    if k == 0 or rows == 0:
+        return out
     o2 = out.reshape(-1, k)
     if o2.stride(-1) != 1 or (rows > 1 and o2.data_ptr() != out.data_ptr()):
         raise ValueError("out must be a contiguous int64 [..., k] tensor")
