@@ -113,13 +113,15 @@ int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, in
 
 /* a6. prefix_scores (splitk.py:582-614, kernel 321-371): per prefix entry j,
  * mass[j] = mean over the G*T2 selection rows of exp(s_rj - mp[r]) / lp[r] (0 on dead
- * slots) and, when value != 0, score[j] = mass[j] * ||v_j - centre|| (0 on dead slots).
+ * slots) and, when value != 0, score[j] = mass[j] * ||v_j - centre|| (0 on dead slots),
+ * centre as ma_value_centre computes it from op (the prefix-only output of
+ * ma_splitk_attention, [B,H,R,D] contiguous, dtype op_dtype; read only when value != 0).
  * v_round_bf16: the distance reads V rounded to bf16 (the reference reads its unpacked
  * bf16 prefix when it has one, splitk.py:513-516, 592).  mass/score [B,H,n] contiguous. */
 int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
-                     const int32_t *q_rows, int T2, const float *mp, const float *lp,
-                     const float *centre, float scale, int value, int v_round_bf16, float *mass,
-                     float *score, void *stream);
+                     const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
+                     int op_dtype, float scale, int value, int v_round_bf16, float *mass, float *score,
+                     void *stream);
 
 /* a9. read-set top-k (session.py:1429-1438, reference.py:369-393): for each of `rows`
  * rows, the k largest of rank[row, 0..n) -- dead slots (mask 0) rank -inf, ties go to
@@ -129,6 +131,48 @@ int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix 
 int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, int64_t mask_stride,
                    int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values,
                    void *stream);
+
+/* a10. keep set of an eviction step (EvictionState.survivors, eviction.py:325-409, for the
+ * score-ranked policies; capacity C = EvictionConfig.capacity, eviction.py:200-202): per
+ * row (one (layer, batch, KV head) lane of n live entries), the W = min(window, C) newest
+ * entries plus the top (C - W) of score among the others, where positions < sink_tokens
+ * and pinned positions [pin_lo, pin_hi) rank +inf (NaN above +inf, ties to the smaller
+ * index), written as C ascending live-axis indices to keep[row*keep_stride + i].
+ * Positions (int32, or int64 when pos_is_i64) must increase strictly along each row --
+ * the state keeps its live arrays in position order -- so index order is position order
+ * and the newest W are the last W; status (optional, int32 [rows]) gets 1 for a row that
+ * breaks this.  pin_lo_rows (optional, [rows]) overrides pin_lo per row. */
+int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const float *score,
+                   int64_t score_stride, int rows, int n, int capacity, int window, int64_t sink_tokens,
+                   const int64_t *pin_lo_rows, int64_t pin_lo, int64_t pin_hi, int has_pin, int64_t *keep,
+                   int64_t keep_stride, int32_t *status, void *stream);
+
+/* a8. value_score (session.py:27-40): score[row, j] = a[row, j] * ||v_j - c||,
+ * c = sum_j w_j v_j / max(sum_j w_j, 1e-12), rows = (b, h) of v [B,H,n,D] (strides b, h, n;
+ * bf16, f16 or f32).  fp32_mode 0 (the reference default): w = bf16(a) and every step in
+ * bf16 arithmetic as the reference's bf16 tensors compute it; fp32_mode 1: the f32 branch
+ * (BITSIEVE_VSCORE_FP32).  a, score [rows, n] with row strides.  D <= 128, D % 8 == 0. */
+int64_t ma_value_score_workspace_bytes(int rows, int n, int D);
+int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, int B, int H, int n, int D, int fp32_mode,
+                   float *score, int64_t score_stride, void *workspace, int64_t workspace_bytes,
+                   void *stream);
+
+/* a13. compaction of survivors (PackedKVCache.compact, cache.py:342-367; compact_tokens,
+ * cache.py:659-678; EvictionState.compact, eviction.py:411-418): for every lane (b, h) and
+ * i < capacity, row i of each plane becomes the old row keep[b, h, i] -- in place, for any
+ * keep (out-of-range entries give zero rows).  A plane p is a token-major tensor: base
+ * bases[p] (element b=0, h=0, token 0), byte strides strides[3p..3p+2] (b, h, token) and
+ * row_bytes[p] bytes per token (even).  keep int64 with strides skeep (b, h; entries
+ * contiguous).  Up to 8 planes per call. */
+int64_t ma_compact_workspace_bytes(int rows, int capacity, const int32_t *row_bytes, int nplanes);
+int ma_compact_tokens(void *const *bases, const int64_t *strides, const int32_t *row_bytes, int nplanes, int B,
+                      int H, int n, const int64_t *keep, const int64_t skeep[2], int capacity, void *workspace,
+                      int64_t workspace_bytes, void *stream);
+
+/* a14. append of a finalized block into a 16-bit cache (PackedKVCache.stage_layer for
+ * bf16 layouts, cache.py:423-547): dst[b, h, at + t, :] = src[b, h, t, :] for t < T,
+ * converted to dst's dtype (round to nearest even). */
+int ma_append_tokens(ma_tensor4 src, ma_tensor4 dst, int B, int H, int T, int D, int at, void *stream);
 
 /* a11. gather_packed_kv (ops.py:570-662, 835-855; oracle reference.py:396-400): the
  * entries idx[b,h,0..k) of the prefix, dequantized, into k_out / v_out [B,H,k,D]

@@ -63,8 +63,14 @@ SIGNATURES = {
     "ma_splitk_partial": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _T4, _T4, _I, _I, _I, _I, _F, _I, _P, _I64, _P]),
     "ma_splitk_merge": (_I, [_I, _I, _I, _I, _I, _I, _I, _T4, _P, _P, _P, _P, _I64, _P]),
     "ma_value_centre": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P]),
-    "ma_prefix_scores": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _P, _I, _P, _P, _P, _F, _I, _I, _P,
+    "ma_prefix_scores": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _P, _I, _P, _P, _P, _I, _F, _I, _I, _P,
                               _P, _P]),
+    "ma_keep_select": (_I, [_P, _I, _I64, _P, _I64, _I, _I, _I, _I, _I64, _P, _I64, _I64, _I, _P, _I64, _P, _P]),
+    "ma_value_score_workspace_bytes": (_I64, [_I, _I, _I]),
+    "ma_value_score": (_I, [_P, _I64, _T4, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P]),
+    "ma_compact_workspace_bytes": (_I64, [_I, _I, _P, _I]),
+    "ma_compact_tokens": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _I64P, _I, _P, _I64, _P]),
+    "ma_append_tokens": (_I, [_T4, _T4, _I, _I, _I, _I, _I, _P]),
     "ma_topk_select": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P, _P]),
     "ma_gather_kv": (_I, [_PREF, _I, _I, _I, _P, _I64P, _I, _T4, _T4, _P]),
     "ma_quantize_keys": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),

@@ -20,11 +20,51 @@ namespace {
 constexpr int MAX_WAVES = NT / 64;
 enum { SRC_PACKED = 0, SRC_DENSE = 1 };
 
+// centre[b,h,:] = mean over rows g*T + q_rows[t2] of f32(op): NTH threads as D channels
+// x (NTH/D) row slices, each slice summing its rows in order, then the slices in order --
+// one fixed summation order, shared by the score kernel's prologue and ma_value_centre.
+template <int D, int NTH>
+__device__ __forceinline__ float centre_partial(const void *op, int op_dtype, int bh, int G, int T,
+                                                const int32_t *q_rows, int T2, int tid) {
+    constexpr int SL = NTH / D;
+    const int d = tid % D, sl = tid / D;
+    const int R = G * T, R2 = G * T2;
+    float s = 0.f;
+    // one loop per dtype: no branch around the loads, which can then all be in flight
+    if (op_dtype == MA_F32) {
+        const float *o = (const float *)op;
+#pragma unroll 8
+        for (int rr = sl; rr < R2; rr += SL) {
+            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
+            s += o[((int64_t)bh * R + row) * D + d];
+        }
+    } else {
+        const uint16_t *o = (const uint16_t *)op;
+        const bool bf = op_dtype == MA_BF16;
+#pragma unroll 8
+        for (int rr = sl; rr < R2; rr += SL) {
+            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
+            const uint16_t x = o[((int64_t)bh * R + row) * D + d];
+            s += bf ? ma_bf16_to_f32(x) : ma_f16_to_f32(x);
+        }
+    }
+    return s;
+}
+
+template <int D, int NTH>
+__device__ __forceinline__ float centre_combine(const float *part, int d, int R2) {
+    float t = 0.f;
+    for (int k = 0; k < NTH / D; ++k) t += part[k * D + d];
+    return t / (float)R2;
+}
+
 struct ScoreArgs {
     ma_tensor4 q;
     PrefixDev pre;
     const int32_t *q_rows;
-    const float *mp, *lp, *centre;
+    const float *mp, *lp;
+    const void *op;  // prefix-only output [B*H, R, D] (op_dtype): the value centre's source
+    int op_dtype;
     float *mass, *score;
     int H, G, T, T2, R, R2, row_tiles, tiles_per_wg, value, vround;
     float sl2;
@@ -93,8 +133,14 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     const bool value = a.value, vround = a.vround;
     const float sl2 = a.sl2;
 
-    if (value)
-        for (int d = tid; d < D; d += NT) cen[d] = a.centre[(int64_t)bh * D + d];
+    if (value) {
+        // centre = mean of O_p over the selection rows, in one fixed order per workgroup
+        float *part = &red[0][0];
+        part[tid] = centre_partial<D, NT>(a.op, a.op_dtype, bh, a.G, a.T, a.q_rows, a.T2, tid);
+        __syncthreads();
+        if (tid < D) cen[tid] = centre_combine<D, NT>(part, tid, a.G * a.T2);
+        __syncthreads();
+    }
     for (int it = tid; it < MAX_WAVES * TILE; it += NT) red[it / TILE][it % TILE] = 0.f;
 
     // Q fragments (A operand) and per-row statistics of this wave's row tiles
@@ -255,41 +301,14 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     }
 }
 
-// centre[b,h,:] = mean over rows g*T + q_rows[t2] of f32(op); grid B*H, 1024 threads:
-// D channels x (1024/D) row slices summed in a fixed order, so the result is
-// deterministic.
-__global__ void __launch_bounds__(1024) centre_kernel(const void *op, int op_dtype, int G, int T, int D,
-                                                      const int32_t *q_rows, int T2, float *centre) {
-    __shared__ float part[1024];
+template <int D>
+__global__ void __launch_bounds__(NT) centre_kernel(const void *op, int op_dtype, int G, int T,
+                                                    const int32_t *q_rows, int T2, float *centre) {
+    __shared__ float part[NT];
     const int bh = blockIdx.x, tid = threadIdx.x;
-    const int slices = 1024 / D, d = tid % D, sl = tid / D;
-    const int R = G * T, R2 = G * T2;
-    float s = 0.f;
-    // one loop per dtype: no branch around the loads, which can then all be in flight
-    if (op_dtype == MA_F32) {
-        const float *o = (const float *)op;
-#pragma unroll 8
-        for (int rr = sl; rr < R2; rr += slices) {
-            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
-            s += o[((int64_t)bh * R + row) * D + d];
-        }
-    } else {
-        const uint16_t *o = (const uint16_t *)op;
-        const bool bf = op_dtype == MA_BF16;
-#pragma unroll 8
-        for (int rr = sl; rr < R2; rr += slices) {
-            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
-            const uint16_t x = o[((int64_t)bh * R + row) * D + d];
-            s += bf ? ma_bf16_to_f32(x) : ma_f16_to_f32(x);
-        }
-    }
-    part[tid] = s;
+    part[tid] = centre_partial<D, NT>(op, op_dtype, bh, G, T, q_rows, T2, tid);
     __syncthreads();
-    if (sl == 0) {
-        float t = 0.f;
-        for (int k = 0; k < slices; ++k) t += part[k * D + d];
-        centre[(int64_t)bh * D + d] = t / (float)R2;
-    }
+    if (tid < D) centre[(int64_t)bh * D + tid] = centre_combine<D, NT>(part, tid, G * T2);
 }
 
 }  // namespace
@@ -302,19 +321,23 @@ extern "C" int ma_value_centre(const void *op, int op_dtype, int B, int H, int G
         ma_set_error("ma_value_centre: bad arguments");
         return MA_EINVAL;
     }
-    hipLaunchKernelGGL(centre_kernel, dim3(B * H), dim3(1024), 0, (hipStream_t)stream, op, op_dtype, G, T, D, q_rows,
-                       T2, centre);
+    if (D == 128)
+        hipLaunchKernelGGL(centre_kernel<128>, dim3(B * H), dim3(NT), 0, (hipStream_t)stream, op, op_dtype, G, T,
+                           q_rows, T2, centre);
+    else
+        hipLaunchKernelGGL(centre_kernel<64>, dim3(B * H), dim3(NT), 0, (hipStream_t)stream, op, op_dtype, G, T,
+                           q_rows, T2, centre);
     return ma_check_launch("ma_value_centre");
 }
 
 extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
-                                const int32_t *q_rows, int T2, const float *mp, const float *lp, const float *centre,
-                                float scale, int value, int v_round_bf16, float *mass, float *score, void *stream) {
+                                const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
+                                int op_dtype, float scale, int value, int v_round_bf16, float *mass, float *score, void *stream) {
     const char *who = "ma_prefix_scores";
     int rc = ma_validate_prefix(p, D, who);
     if (rc) return rc;
     if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || T2 <= 0 || !q.ptr || !q_rows || !mp || !lp || !mass ||
-        (value && (!score || !centre))) {
+        (value && (!score || !op))) {
         ma_set_error("%s: bad sizes or NULL pointer", who);
         return MA_EINVAL;
     }
@@ -341,7 +364,8 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     sa.q_rows = q_rows;
     sa.mp = mp;
     sa.lp = lp;
-    sa.centre = centre;
+    sa.op = op;
+    sa.op_dtype = op_dtype;
     sa.mass = mass;
     sa.score = score;
     sa.H = H;

@@ -1,124 +1,117 @@
-// Per-row top-k selection with index-ascending tie-break (the read set of
-// session.py:1429-1438: rank.masked_fill(dead, -inf).topk(k) followed by an ascending
-// sort of the indices).
+// Per-row selection kernels with index-ascending tie-break:
+//   * read set  (session.py:1429-1438): rank.masked_fill(dead, -inf).topk(k), indices sorted;
+//   * keep set  (eviction.py:355-409, score-ranked policies): the W newest entries, plus the
+//     top (C - W) of the score among the others where sinks and pinned positions rank
+//     +inf, returned in position order.
 //
-// One workgroup (1024 threads) per row; thread i owns the VPT consecutive entries
-// [i*VPT, (i+1)*VPT) as monotone 32-bit keys in registers.  The k-th largest key T is
-// found exactly by a most-significant-bit-first bisection (32 block-wide counts of
-// key >= candidate).  An entry is selected if key > T, or key == T and fewer than
-// k - count(key > T) equal keys precede it in index order; a block-wide exclusive scan
-// of the selection flags, taken in index order, then gives every selected entry its
-// output slot -- the output is ascending by construction, no sort.
+// One workgroup (1024 threads) per row.  Element j = e*NT + tid lives in thread tid, slot
+// e, as a monotone 32-bit key (larger float -> larger key, -0.0 == +0.0, NaN above +inf,
+// padding 0 below every real key).  The k-th largest key T is found exactly by an LDS
+// histogram radix select over three digits (11 + 11 + 10 bits): per digit one pass of LDS
+// atomics over the keys that match the digits found so far, then a block-wide suffix
+// scan of the bins.  An element is selected if key > T, or key == T and fewer than
+// k - count(key > T) equal keys precede it in index order.  A block-wide exclusive scan of
+// the selection flags in index order gives every selected element its output slot, so the
+// output is ascending by construction -- no sort.
 #include "ma_common.h"
 
 namespace {
 
 constexpr int NT = 1024;
 constexpr int NW = NT / 64;
+constexpr int NBINS = 2048;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-// One workgroup per row.  Element j = e*NT + tid belongs to thread tid (slot e), so every
-// load is coalesced and, within a slot, index order is thread order.  Counting uses wave
-// ballots (a popcount per wave, no shuffles); the k-th largest key T is found by a
-// most-significant-bit-first bisection, one barrier per bit (double-buffered counts).
-// Output slot of a selected element = selected elements in earlier slots + in earlier
-// waves of its slot + lanes below it in its wave: ascending indices, no sort.
 template <int VPT>
-__global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t rank_stride, const uint8_t *mask,
-                                                  int64_t mask_stride, int n, int k, int64_t *idx,
-                                                  int64_t idx_stride, float *values) {
-    __shared__ int cnt2[2][NW];
-    __shared__ int c_gt[VPT][NW], c_eq[VPT][NW], c_sel[VPT][NW];
-    __shared__ int p_eq[VPT + 1], p_sel[VPT + 1];
-    static_assert(VPT <= 64, "one wave scans the slots");
-    const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
-    const float *rr = rank + (int64_t)row * rank_stride;
-    const uint8_t *mr = mask ? mask + (int64_t)row * mask_stride : nullptr;
-    uint32_t key[VPT];
-    // branchless loads from clamped indices, so all VPT loads are in flight at once
-    float v[VPT];
+struct SelectSmem {
+    uint32_t hist[NBINS];
+    int wsum[NW];
+    int found_digit, found_gt;
+    int c_eq[VPT][NW], c_sel[VPT][NW];
+    int p_eq[VPT + 1], p_sel[VPT + 1];
+    int flag;
+};
+
+// Block-wide inclusive suffix sum of v over thread order (thread t gets sum over t' >= t).
+template <int VPT>
+__device__ __forceinline__ int block_suffix_incl(int v, SelectSmem<VPT> &S) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int e = 0; e < VPT; ++e) v[e] = rr[min(e * NT + tid, n - 1)];
-    uint32_t live = 0xffffffffu;
-    if (mr) {
-        uint8_t mb[VPT];
-#pragma unroll
-        for (int e = 0; e < VPT; ++e) mb[e] = mr[min(e * NT + tid, n - 1)];
-#pragma unroll
-        for (int e = 0; e < VPT; ++e) v[e] = mb[e] ? v[e] : -INFINITY;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_down(v, o);
+        if (lane + o < 64) v += y;
     }
-    (void)live;
+    if (lane == 0) S.wsum[wave] = v;   // lane 0 holds the wave total
+    __syncthreads();
+    int above = 0;
 #pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const int j = e * NT + tid;
-        key[e] = j < n ? ma_order_key(v[e]) : 0u;  // 0: below every real key (-inf maps to 0x007fffff)
-    }
-    uint32_t thr = 0u;
-    for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = thr | (1u << bit);
-        int c = 0;
-#pragma unroll
-        for (int e = 0; e < VPT; ++e) c += __popcll(__ballot(key[e] >= cand));
-        if (lane == 0) cnt2[bit & 1][wave] = c;
+    for (int w = 0; w < NW; ++w) above += (w > wave) ? S.wsum[w] : 0;
+    return v + above;
+}
+
+// The k-th largest of the block's keys (1 <= k <= number of keys).  Returns T and sets
+// need = k - count(key > T), the number of keys equal to T that are selected.
+template <int VPT>
+__device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT> &S, int &need) {
+    const int tid = threadIdx.x;
+    uint32_t prefix = 0u, pmask = 0u;
+    int kk = k;
+#pragma unroll 1
+    for (int p = 0; p < 3; ++p) {
+        const int shift = p == 0 ? 21 : (p == 1 ? 10 : 0);
+        const int nb = p == 2 ? 1024 : 2048;
+        for (int i = tid; i < NBINS; i += NT) S.hist[i] = 0u;
         __syncthreads();
-        int tot = 0;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) tot += cnt2[bit & 1][w];
-        if (tot >= k) thr = cand;
+        for (int e = 0; e < VPT; ++e)
+            if ((key[e] & pmask) == prefix) atomicAdd(&S.hist[(key[e] >> shift) & (uint32_t)(nb - 1)], 1u);
+        __syncthreads();
+        // thread t owns bins 2t (lower digit) and 2t+1
+        const int b0 = 2 * tid;
+        const int c0 = b0 < nb ? (int)S.hist[b0] : 0;
+        const int c1 = b0 + 1 < nb ? (int)S.hist[b0 + 1] : 0;
+        const int incl = block_suffix_incl<VPT>(c0 + c1, S);
+        const int above = incl - c0 - c1;  // keys with a digit above both of my bins
+        if (above < kk && above + c1 >= kk) {
+            S.found_digit = b0 + 1;
+            S.found_gt = above;
+        } else if (above + c1 < kk && above + c1 + c0 >= kk) {
+            S.found_digit = b0;
+            S.found_gt = above + c1;
+        }
+        __syncthreads();
+        const uint32_t d = (uint32_t)S.found_digit;
+        kk -= S.found_gt;
+        prefix |= d << shift;
+        pmask |= (uint32_t)(nb - 1) << shift;
+        __syncthreads();  // found_* and wsum are rewritten by the next pass
     }
+    need = kk;
+    return prefix;
+}
+
+// Select key > T or (key == T and among the first `need` equal keys in index order), and
+// give every selected element its rank in index order.  Writes slot (or -1) per slot e.
+template <int VPT, class Emit>
+__device__ void select_and_rank(const uint32_t (&key)[VPT], uint32_t thr, int need, SelectSmem<VPT> &S,
+                                Emit emit) {
+    const int wave = threadIdx.x >> 6, lane = lane_id();
     const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-        const uint64_t bg = __ballot(key[e] > thr);
         const uint64_t be = __ballot(key[e] == thr);
-        if (lane == 0) {
-            c_gt[e][wave] = __popcll(bg);
-            c_eq[e][wave] = __popcll(be);
-        }
+        if (lane == 0) S.c_eq[e][wave] = __popcll(be);
     }
     __syncthreads();
-    // wave 0, lane e: slot e's counts -> exclusive prefix over waves (in place) and, by a
-    // wave scan, over slots; the gt total gives the number of equal keys still needed
-    if (wave == 0) {
-        int eq_tot = 0, gt_tot = 0;
-        if (lane < VPT) {
-            for (int w = 0; w < NW; ++w) {
-                const int c = c_eq[lane][w];
-                c_eq[lane][w] = eq_tot;
-                eq_tot += c;
-                gt_tot += c_gt[lane][w];
-            }
-        }
-        int incl = eq_tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
-        }
-        gt_tot = ma_wave_sum_i(gt_tot);
-        if (lane < VPT) p_eq[lane] = incl - eq_tot;
-        if (lane == 0) p_eq[VPT] = k - gt_tot;  // equal keys still needed
-    }
-    __syncthreads();
-    const int need = p_eq[VPT];
-    uint64_t selbits = 0;  // bit e: this thread's slot-e element is selected
-#pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const bool is_eq = key[e] == thr;
-        const int eb = p_eq[e] + c_eq[e][wave] + __popcll(__ballot(is_eq) & below);
-        const bool sl = key[e] > thr || (is_eq && eb < need);
-        selbits |= (uint64_t)sl << e;
-        const uint64_t bs = __ballot(sl);
-        if (lane == 0) c_sel[e][wave] = __popcll(bs);
-    }
-    __syncthreads();
+    // wave 0, lane e: slot e's equal counts -> exclusive prefix over waves (in place) and,
+    // by a wave scan, over slots
     if (wave == 0) {
         int tot = 0;
         if (lane < VPT) {
             for (int w = 0; w < NW; ++w) {
-                const int c = c_sel[lane][w];
-                c_sel[lane][w] = tot;
+                const int c = S.c_eq[lane][w];
+                S.c_eq[lane][w] = tot;
                 tot += c;
             }
         }
@@ -128,22 +121,151 @@ __global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t ran
             const int y = __shfl_up(incl, o);
             if (lane >= o) incl += y;
         }
-        if (lane < VPT) p_sel[lane] = incl - tot;
+        if (lane < VPT) S.p_eq[lane] = incl - tot;
     }
     __syncthreads();
-    int64_t *out = idx + (int64_t)row * idx_stride;
-    float *vout = values ? values + (int64_t)row * k : nullptr;
+    uint64_t selbits = 0;
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+        const bool is_eq = key[e] == thr;
+        const int eb = S.p_eq[e] + S.c_eq[e][wave] + __popcll(__ballot(is_eq) & below);
+        const bool sl = key[e] > thr || (is_eq && eb < need);
+        selbits |= (uint64_t)sl << e;
+        const uint64_t bs = __ballot(sl);
+        if (lane == 0) S.c_sel[e][wave] = __popcll(bs);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int tot = 0;
+        if (lane < VPT) {
+            for (int w = 0; w < NW; ++w) {
+                const int c = S.c_sel[lane][w];
+                S.c_sel[lane][w] = tot;
+                tot += c;
+            }
+        }
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        if (lane < VPT) S.p_sel[lane] = incl - tot;
+    }
+    __syncthreads();
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
         const bool sl = (selbits >> e) & 1;
         const uint64_t bs = __ballot(sl);
-        const int slot = p_sel[e] + c_sel[e][wave] + __popcll(bs & below);
-        if (sl && slot < k) {
+        if (sl) emit(e, S.p_sel[e] + S.c_sel[e][wave] + __popcll(bs & below));
+    }
+}
+
+// ---------------------------------------------------------------- read set
+template <int VPT>
+__global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t rank_stride, const uint8_t *mask,
+                                                  int64_t mask_stride, int n, int k, int64_t *idx,
+                                                  int64_t idx_stride, float *values) {
+    __shared__ SelectSmem<VPT> S;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *rr = rank + (int64_t)row * rank_stride;
+    const uint8_t *mr = mask ? mask + (int64_t)row * mask_stride : nullptr;
+    uint32_t key[VPT];
+    // branchless loads from clamped indices, 16 slots at a time in flight
+#pragma unroll
+    for (int e0 = 0; e0 < VPT; e0 += 16) {
+        constexpr int CH = VPT < 16 ? VPT : 16;
+        float v[CH];
+        uint8_t mb[CH];
+#pragma unroll
+        for (int e = 0; e < CH; ++e) v[e] = rr[min((e0 + e) * NT + tid, n - 1)];
+#pragma unroll
+        for (int e = 0; e < CH; ++e) mb[e] = mr ? mr[min((e0 + e) * NT + tid, n - 1)] : (uint8_t)1;
+#pragma unroll
+        for (int e = 0; e < CH; ++e)
+            key[e0 + e] = (e0 + e) * NT + tid < n ? ma_order_key(mb[e] ? v[e] : -INFINITY) : 0u;
+    }
+    int need;
+    const uint32_t thr = radix_kth<VPT>(key, k, S, need);
+    int64_t *out = idx + (int64_t)row * idx_stride;
+    float *vout = values ? values + (int64_t)row * k : nullptr;
+    select_and_rank<VPT>(key, thr, need, S, [&](int e, int slot) {
+        if (slot < k) {
             const int j = e * NT + tid;
             out[slot] = j;
-            if (vout) vout[slot] = v[e];
+            if (vout) vout[slot] = (mr && !mr[j]) ? -INFINITY : rr[j];
+        }
+    });
+}
+
+// ---------------------------------------------------------------- keep set
+// Row = one (layer, batch, KV head) lane with n live entries whose positions increase
+// strictly along the live axis (the eviction state's invariant: survivors are stored in
+// position order and new entries are appended with larger positions).  Then the W newest
+// entries are the last W, the contest runs over the first m = n - W entries, and index
+// order is position order.  A row whose positions do not increase gets status 1.
+template <int VPT, typename PosT>
+__global__ void __launch_bounds__(NT) keep_kernel(const PosT *pos, int64_t pos_stride, const float *score,
+                                                  int64_t score_stride, int n, int capacity, int window,
+                                                  int64_t sink_tokens, const int64_t *pin_lo_rows, int64_t pin_lo,
+                                                  int64_t pin_hi, int has_pin, int64_t *keep, int64_t keep_stride,
+                                                  int32_t *status) {
+    __shared__ SelectSmem<VPT> S;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const PosT *pr = pos + (int64_t)row * pos_stride;
+    const float *sr = score + (int64_t)row * score_stride;
+    const int w = min(window, capacity);
+    const int m = n - w;         // contestants
+    const int rest = capacity - w;
+    const int64_t plo = pin_lo_rows ? pin_lo_rows[row] : pin_lo;
+    if (tid == 0) S.flag = 0;
+    __syncthreads();
+    uint32_t key[VPT];
+    bool bad = false;
+#pragma unroll
+    for (int e0 = 0; e0 < VPT; e0 += 8) {
+        constexpr int CH = VPT < 8 ? VPT : 8;
+        PosT p[CH], pn[CH];
+        float v[CH];
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int jc = min((e0 + e) * NT + tid, n - 1);
+            p[e] = pr[jc];
+            pn[e] = pr[min(jc + 1, n - 1)];
+            v[e] = sr[jc];
+        }
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int j = (e0 + e) * NT + tid;
+            bad |= (j + 1 < n) && !(p[e] < pn[e]);
+            float x = v[e];
+            if ((int64_t)p[e] < sink_tokens) x = INFINITY;
+            if (has_pin && (int64_t)p[e] >= plo && (int64_t)p[e] < pin_hi) x = INFINITY;
+            key[e0 + e] = j < m ? ma_order_key(x) : 0u;
         }
     }
+    if (bad) S.flag = 1;   // benign race: every writer stores 1
+    __syncthreads();
+    if (tid == 0 && status) status[row] = S.flag;
+    int64_t *out = keep + (int64_t)row * keep_stride;
+    if (rest > 0) {
+        int need;
+        const uint32_t thr = radix_kth<VPT>(key, rest, S, need);
+        select_and_rank<VPT>(key, thr, need, S, [&](int e, int slot) {
+            if (slot < rest) out[slot] = e * NT + tid;
+        });
+    }
+    for (int i = tid; i < w; i += NT) out[rest + i] = m + i;
+}
+
+int vpt_for(int n) {
+    const int v = (n + NT - 1) / NT;
+    if (v <= 4) return 4;
+    if (v <= 8) return 8;
+    if (v <= 16) return 16;
+    if (v <= 32) return 32;
+    if (v <= 64) return 64;
+    return 0;
 }
 
 }  // namespace
@@ -157,19 +279,58 @@ extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint
     }
     if (rows == 0 || k == 0) return MA_OK;
     hipStream_t st = (hipStream_t)stream;
-    const int vpt = (n + NT - 1) / NT;
+    const int vpt = vpt_for(n);
 #define MA_TOPK(V)                                                                                                \
     hipLaunchKernelGGL(topk_kernel<V>, dim3(rows), dim3(NT), 0, st, rank, rank_stride, mask, mask_stride, n, k, idx, \
                        idx_stride, values)
-    if (vpt <= 4) MA_TOPK(4);
-    else if (vpt <= 8) MA_TOPK(8);
-    else if (vpt <= 16) MA_TOPK(16);
-    else if (vpt <= 32) MA_TOPK(32);
-    else if (vpt <= 64) MA_TOPK(64);
-    else {
-        ma_set_error("ma_topk_select: n=%d exceeds the built maximum %d", n, 64 * NT);
-        return MA_EUNSUPPORTED;
+    switch (vpt) {
+        case 4: MA_TOPK(4); break;
+        case 8: MA_TOPK(8); break;
+        case 16: MA_TOPK(16); break;
+        case 32: MA_TOPK(32); break;
+        case 64: MA_TOPK(64); break;
+        default:
+            ma_set_error("ma_topk_select: n=%d exceeds the built maximum %d", n, 64 * NT);
+            return MA_EUNSUPPORTED;
     }
 #undef MA_TOPK
     return ma_check_launch("ma_topk_select");
+}
+
+extern "C" int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const float *score,
+                              int64_t score_stride, int rows, int n, int capacity, int window, int64_t sink_tokens,
+                              const int64_t *pin_lo_rows, int64_t pin_lo, int64_t pin_hi, int has_pin, int64_t *keep,
+                              int64_t keep_stride, int32_t *status, void *stream) {
+    if (!pos || !score || !keep || rows < 0 || n < 0 || capacity < 0 || capacity > n || window < 0 ||
+        keep_stride < capacity || pos_stride < n || score_stride < n) {
+        ma_set_error("ma_keep_select: bad arguments (rows=%d n=%d capacity=%d window=%d)", rows, n, capacity,
+                     window);
+        return MA_EINVAL;
+    }
+    if (rows == 0 || capacity == 0) return MA_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const int vpt = vpt_for(n);
+#define MA_KEEP(V)                                                                                                  \
+    do {                                                                                                            \
+        if (pos_is_i64)                                                                                             \
+            hipLaunchKernelGGL((keep_kernel<V, int64_t>), dim3(rows), dim3(NT), 0, st, (const int64_t *)pos,         \
+                               pos_stride, score, score_stride, n, capacity, window, sink_tokens, pin_lo_rows, pin_lo, \
+                               pin_hi, has_pin, keep, keep_stride, status);                                          \
+        else                                                                                                        \
+            hipLaunchKernelGGL((keep_kernel<V, int32_t>), dim3(rows), dim3(NT), 0, st, (const int32_t *)pos,         \
+                               pos_stride, score, score_stride, n, capacity, window, sink_tokens, pin_lo_rows, pin_lo, \
+                               pin_hi, has_pin, keep, keep_stride, status);                                          \
+    } while (0)
+    switch (vpt) {
+        case 4: MA_KEEP(4); break;
+        case 8: MA_KEEP(8); break;
+        case 16: MA_KEEP(16); break;
+        case 32: MA_KEEP(32); break;
+        case 64: MA_KEEP(64); break;
+        default:
+            ma_set_error("ma_keep_select: n=%d exceeds the built maximum %d", n, 64 * NT);
+            return MA_EUNSUPPORTED;
+    }
+#undef MA_KEEP
+    return ma_check_launch("ma_keep_select");
 }

@@ -204,17 +204,15 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
     score = torch.empty_like(mass) if value else None
     lib = N.load()
     st = N.stream_of(query)
-    centre = None
-    if value:
-        centre = torch.empty((b, hkv, d), device=query.device, dtype=torch.float32)
-        N.check(lib.ma_value_centre(op.data_ptr(), N.dtype_code(op.dtype), b, hkv, g, t, d, q_rows.data_ptr(), t2,
-                                    centre.data_ptr(), st), "ma_value_centre")
     if n == 0:
         return mass, score
+    if value and (not op.is_contiguous() or tuple(op.shape) != (b, hkv, g * t, d)):
+        raise ValueError("stats O_p must be a contiguous [B, Hkv, R, D] tensor")
     scale = float(scaling) if scaling is not None else d ** -0.5
     vround = 1 if (prefix.nq and prefix.vround) else 0
     rc = lib.ma_prefix_scores(N.t4(query), b, hq, t, d, prefix.native(), hkv, q_rows.data_ptr(), t2,
-                              mp.data_ptr(), lp.data_ptr(), N.ptr(centre), scale, 1 if value else 0, vround,
+                              mp.data_ptr(), lp.data_ptr(), op.data_ptr() if value else None,
+                              N.dtype_code(op.dtype) if value else 0, scale, 1 if value else 0, vround,
                               mass.data_ptr(), N.ptr(score), st)
     N.check(rc, "ma_prefix_scores")
     return mass, score
