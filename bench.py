@@ -159,7 +159,7 @@ def main():
     # the dominant kernel alone: split-K pass 1 (same arguments, its own graph)
     lib = N.load()
     hq, t, d, hkv = sh.hq, sh.t, sh.d, sh.hkv
-    ws_bytes = int(lib.ma_splitk_workspace_bytes(sh.b, hkv, hq, t, d, sh.n, a.split_tokens))
+    ws_bytes = int(lib.ma_splitk_workspace_bytes(sh.b, hkv, hq, t, d, sh.n, 0, a.split_tokens))
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     pre_native = prefix.native()
     qt, kct, vct = N.t4(qg), N.t4(kcg), N.t4(vcg)

@@ -86,21 +86,23 @@ int ma_dequant_prefix(const ma_prefix *p, int B, int H, int D, ma_tensor4 k_out,
                       void *stream);
 
 /* a4 + a5. splitk_attention (splitk.py:493-579): softmax over [prefix | current] for all
- * R = (Hq/H)*T rows of every KV head.  Pass 1 writes per-split partials (max, sum, acc)
- * into `workspace`, pass 2 merges them (log-sum-exp) into `out` [B,Hq,T,D] and, when mp
- * is not NULL, the prefix-only statistics mp, lp f32 [B,H,R] (contiguous) and op
- * [B,H,R,D] (contiguous, dtype of out).  causal_block > 0: current key j is visible to
- * query t only if (c_pos0+j)/causal_block <= (q_pos0+t)/causal_block.
- * split_tokens: prefix tokens per split (multiple of 64; 0 = library default). */
-int64_t ma_splitk_workspace_bytes(int B, int H, int Hq, int T, int D, int n, int split_tokens);
+ * R = (Hq/H)*T rows of every KV head.  Pass 1 writes per-split partials (max, sum and the
+ * normalized output on a per-row f16 scale) into `workspace`, pass 2 merges them
+ * (log-sum-exp) into `out` [B,Hq,T,D] and, when mp is not NULL, the prefix-only
+ * statistics mp, lp f32 [B,H,R] (contiguous) and op [B,H,R,D] (contiguous, dtype of out).
+ * causal_block > 0: current key j is visible to query t only if
+ * (c_pos0+j)/causal_block <= (q_pos0+t)/causal_block.  split_tokens: prefix tokens per
+ * split (multiple of 64; 0 = library default).  The workspace size depends on the packed
+ * (nq) and 16-bit (nf) prefix lengths. */
+int64_t ma_splitk_workspace_bytes(int B, int H, int Hq, int T, int D, int nq, int nf, int split_tokens);
 /* The two passes of ma_splitk_attention as separate launches (same arguments and
  * workspace): ma_splitk_partial writes the per-split partials (_sk_fwd, splitk.py:116-190),
- * ma_splitk_merge merges them (_sk_combine, splitk.py:272-318); n = prefix length. */
+ * ma_splitk_merge merges them (_sk_combine, splitk.py:272-318). */
 int ma_splitk_partial(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H, ma_tensor4 kc,
                       ma_tensor4 vc, int Tc, int causal_block, int q_pos0, int c_pos0, float scale,
                       int split_tokens, void *workspace, int64_t workspace_bytes, void *stream);
-int ma_splitk_merge(int B, int Hq, int T, int D, int H, int n, int split_tokens, ma_tensor4 out, float *mp,
-                    float *lp, void *op, void *workspace, int64_t workspace_bytes, void *stream);
+int ma_splitk_merge(int B, int Hq, int T, int D, int H, int nq, int nf, int split_tokens, ma_tensor4 out,
+                    float *mp, float *lp, void *op, void *workspace, int64_t workspace_bytes, void *stream);
 int ma_splitk_attention(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
                         ma_tensor4 kc, ma_tensor4 vc, int Tc, int causal_block, int q_pos0,
                         int c_pos0, float scale, ma_tensor4 out, float *mp, float *lp, void *op,

@@ -1,27 +1,35 @@
 // Split-K (flash-decoding) attention over [prefix | current block] for every query row
 // of a KV head's GQA group (the reference's splitk_attention, splitk.py:493-579).
 //
-// Pass 1 (splitk_fwd_kernel): grid (nsplit + 1, B*H, row groups).  Workgroup = one
-// prefix split (or, for blockIdx.x == nsplit, the current block) x up to 8 row tiles of
-// 32 query rows, one wave per row tile.  Per 64-token tile the workgroup stages K as
-// Ks[t][d] and V as Vt[d][t] (bf16, dequantized in the load path for packed caches) in
-// LDS; each wave then computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows,
-// B = Q^T held in registers), so every lane owns ONE query row and a strip of 16 tokens
-// per 32-token sub-tile: the row max needs one cross-half exchange, no shuffle trees.
-// The exponentiated S^T registers are the B operand of O^T += V^T P^T directly (the
-// token order of the MFMA's K index is permuted consistently on both operands), and the
-// O^T accumulator keeps the lane's row too, so the online-softmax rescale is per lane.
+// Pass 1 (splitk_fwd_kernel): one workgroup = one (batch, KV head) lane x one token range
+// (a prefix split, or the current block) x up to 7 row tiles of 32 query rows; 16 waves
+// with fixed roles, software-pipelined over 64-token tiles with one barrier per tile:
+//   S waves 0..6     S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
+//                    B = Q^T held in registers), so a lane owns ONE query row and 16
+//                    tokens of each 32-token half; online softmax with a lazily raised
+//                    reference max; the probabilities P^T (bf16) go to LDS exactly in the
+//                    register order the PV MFMA consumes, plus a per-row rescale factor.
+//   O waves 8..14    one tile behind: O^T = alpha * O^T + V^T P^T (A = V^T from LDS,
+//                    B = P^T from LDS); the accumulator keeps the lane's row.
+//   waves 7..15      staging: K lanes dequantize tile i+1 into the K buffer and prefetch
+//                    tile i+2; V lanes dequantize tile i into the V buffer and prefetch
+//                    tile i+1 (V is consumed one iteration later than K).
+// K, V and P are double-buffered; every wave holds at most ~128 VGPRs, so the 16 waves
+// fit 4 per SIMD and the MFMA work of one wave overlaps the VALU work of the others.
 // Pass 2 (splitk_combine_kernel): log-sum-exp merge of the partials into the output and
 // the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
 #include <type_traits>
 
-#include "ma_tile.h"
+#include "ma_stage.h"
 
 using namespace ma;
 
 namespace {
 
-constexpr int MAX_WAVES = NT / 64;
+constexpr int NTH = 1024;
+constexpr int MAXS = 7;                     // row tiles (S/O wave pairs) per workgroup
+constexpr int NSTAGE = 9 * 64;              // staging lanes: waves 7..15
+constexpr int KLANES = NSTAGE / 2;          // K lanes, then as many V lanes
 // a row's running reference max is raised only when a tile's max exceeds it by more than
 // 2^8 in exp2 units, so most tiles skip the accumulator rescale; p <= 2^8 stays exact
 constexpr float LAZY_LOG2 = 8.0f;
@@ -30,54 +38,104 @@ struct FwdArgs {
     ma_tensor4 q;
     PrefixDev pre;
     ma_tensor4 kc, vc;
-    int H, G, T, R, Tc, nsplit, split_n, causal, q_pos0, c_pos0, row_tiles;
+    int H, G, T, R, Tc, nsplit, split_n, causal, q_pos0, c_pos0, row_tiles, row_groups, BH;
+    // this launch: splits [0, nsp) of its token range [tok_beg, tok_end) of every lane,
+    // written to slots slot0 + split; with_cur: the current-block workgroups follow
+    int nsp, slot0, tok_beg, tok_end, with_cur;
     float sl2;  // scale * log2(e)
     float scale;
-    float *wm, *wl, *wacc;  // partials [B*H][nsplit+1][R] and [..][R][D]
-};
-
-// Online-softmax state of one query row (the lane's column of S^T); l and acc are
-// relative to m_ref, m_true is the exact running max (raw logit units).
-template <int D>
-struct RowState {
-    float m_ref, m_true, l;
-    f32x16_t acc[D / 32];
+    // partials of every (lane, slot, row), slot = split or nsplit (current block):
+    // wm = row max (natural-log units), wl = sum of exp relative to it, wsc = scale and
+    // wo = f16(O / scale), O = the slot's normalized output (wo * wsc); wo [..][R][D]
+    float *wm, *wl, *wsc;
+    _Float16 *wo;
 };
 
 template <int D>
-__device__ __forceinline__ void row_reset(RowState<D> &st) {
-    st.m_ref = -INFINITY;
-    st.m_true = -INFINITY;
-    st.l = 0.f;
+struct FwdSmem {
+    KTileL<D> kt[2];
+    VTileL<D> vt[2];
+    uint4 p[2][MAXS][4][64];   // P^T fragments: [buffer][S wave][16-token chunk][lane]
+    float alpha[2][MAXS][32];  // rescale factor of each row, when resc is set
+    int resc[2][MAXS];
+    uint64_t kmask[2];         // usable tokens of the K tile in each buffer
+    float fin[MAXS][3][32];    // final m_ref, m_true, l of every row
+};
+
+// write a row's partial: max in natural-log units, the sum of exp relative to it, and the
+// normalized output O = acc / l as f16 on a per-row scale (the row's max |O|), so the
+// partial is half the size of an f32 one and cannot overflow.
+template <int D>
+__device__ __forceinline__ void write_partial(const FwdArgs &a, const f32x16_t *acc, float m_ref, float m_true,
+                                              float l, int bh, int slot, int row, int hf) {
+    constexpr int NDT = D / 32;
+    const int64_t prow = ((int64_t)bh * (a.nsplit + 1) + slot) * a.R + row;
+    float mx = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) st.acc[dt] = f32x16_t{};
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(acc[dt][i]));
+    mx = ma_max_xor32(mx);                       // the row's other half lives in lane ^ 32
+    const float inv = mx > 0.f ? 1.0f / mx : 0.f;
+    if (hf == 0) {
+        float f = 0.f;
+        if (m_true != -INFINITY) f = __builtin_amdgcn_exp2f((m_ref - m_true) * a.sl2);
+        a.wm[prow] = m_true * a.scale;
+        a.wl[prow] = l * f;
+        a.wsc[prow] = l > 0.f ? mx / l : 0.f;    // O = acc / l = wo * wsc
+    }
+    _Float16 *dst = a.wo + prow * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
+            const f16x4_t v = {(_Float16)(acc[dt][q4 * 4 + 0] * inv), (_Float16)(acc[dt][q4 * 4 + 1] * inv),
+                               (_Float16)(acc[dt][q4 * 4 + 2] * inv), (_Float16)(acc[dt][q4 * 4 + 3] * inv)};
+            *(f16x4_t *)&dst[dt * 32 + q4 * 8 + hf * 4] = v;
+        }
 }
 
-// One 64-token tile for a wave's 32 rows: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// S wave: S^T = K Q^T for one 64-token tile (A = K rows from LDS, B = Q^T in registers).
+// K fragments are loaded one k-step ahead of the MFMAs; the two token halves alternate,
+// so consecutive MFMAs never wait on each other's accumulator.
 template <int D>
-__device__ __forceinline__ void attend_tile(const TileLds<D> &L, const bf16x8_t *qf, RowState<D> &st, int c32, int hf,
-                                            bool need_mask, int lim, float sl2) {
-    constexpr int KS = TileLds<D>::KS, VS = TileLds<D>::VS;
-    constexpr int NKS = D / 16, NDT = D / 32;
-    f32x16_t s[2];
+__device__ __forceinline__ void s_qk(const uint16_t *K, const bf16x8_t *qf, int c32, int hf, f32x16_t *s) {
+    constexpr int KS = D + 8;
+    constexpr int NKS = D / 16;
+    s[0] = f32x16_t{};
+    s[1] = f32x16_t{};
+    const uint16_t *k0 = &K[c32 * KS + hf * 8];
+    const uint16_t *k1 = &K[(32 + c32) * KS + hf * 8];
+    bf16x8_t ka0 = *(const bf16x8_t *)k0, ka1 = *(const bf16x8_t *)k1;
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-        s[t2] = f32x16_t{};
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            const bf16x8_t ka = *(const bf16x8_t *)&L.k[(t2 * 32 + c32) * KS + ks * 16 + hf * 8];
-            s[t2] = ma_mfma32(ka, qf[ks], s[t2]);
+    for (int ks = 0; ks < NKS; ++ks) {
+        bf16x8_t na0 = ka0, na1 = ka1;
+        if (ks + 1 < NKS) {
+            na0 = *(const bf16x8_t *)(k0 + (ks + 1) * 16);
+            na1 = *(const bf16x8_t *)(k1 + (ks + 1) * 16);
         }
+        s[0] = ma_mfma32(ka0, qf[ks], s[0]);
+        s[1] = ma_mfma32(ka1, qf[ks], s[1]);
+        ka0 = na0;
+        ka1 = na1;
     }
+}
+
+// S wave: online softmax of one tile's S^T, P^T (bf16) and the rescale factor to LDS.
+template <int D>
+__device__ __forceinline__ void s_softmax(f32x16_t *s, uint64_t okm, float &m_ref, float &m_true, float &l, int c32,
+                                          int hf, int lane, bool need_mask, int lim, float sl2, uint4 *pdst,
+                                          float *adst, int *rdst) {
     // element i of s[t2] <-> token t2*32 + (i/4)*8 + hf*4 + i%4
     if (need_mask) {
-        const uint64_t okm = L.okmask >> (hf * 4);
+        const uint64_t okh = okm >> (hf * 4);
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int tk = t2 * 32 + (i >> 2) * 8 + (i & 3);
-                const bool ok = ((okm >> tk) & 1) && tk < lim;
+                const bool ok = ((okh >> tk) & 1) && tk < lim;
                 s[t2][i] = ok ? s[t2][i] : -INFINITY;
             }
     }
@@ -87,17 +145,19 @@ __device__ __forceinline__ void attend_tile(const TileLds<D> &L, const bf16x8_t 
 #pragma unroll
         for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[t2][i]);
     mt = ma_max_xor32(mt);
-    st.m_true = fmaxf(st.m_true, mt);
-    const bool need = (mt - st.m_ref) * sl2 > LAZY_LOG2;   // false for NaN (both -inf)
+    m_true = fmaxf(m_true, mt);
+    const bool need = (mt - m_ref) * sl2 > LAZY_LOG2;   // false for NaN (both -inf)
     if (__any(need)) {
-        const float m_new = need ? mt : st.m_ref;
-        const float alpha = (m_new == st.m_ref) ? 1.0f : __builtin_amdgcn_exp2f((st.m_ref - m_new) * sl2);
-        st.l *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) st.acc[dt] *= alpha;
-        st.m_ref = m_new;
+        const float m_new = need ? mt : m_ref;
+        const float alpha = (m_new == m_ref) ? 1.0f : __builtin_amdgcn_exp2f((m_ref - m_new) * sl2);
+        l *= alpha;
+        m_ref = m_new;
+        if (hf == 0) adst[c32] = alpha;
+        if (lane == 0) *rdst = 1;
+    } else if (lane == 0) {
+        *rdst = 0;
     }
-    const float off = (st.m_ref == -INFINITY) ? 0.f : -st.m_ref * sl2;
+    const float off = (m_ref == -INFINITY) ? 0.f : -m_ref * sl2;
     float ls = 0.f;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
@@ -107,207 +167,372 @@ __device__ __forceinline__ void attend_tile(const TileLds<D> &L, const bf16x8_t 
             s[t2][i] = p;
             ls += p;
         }
-    st.l += ma_sum_xor32(ls);
-    // P^T chunks (B operand): chunk c = 16 tokens, lane holds s[c/2][8*(c%2) .. +7]
-    bf16x8_t pb[4];
+    l += ma_sum_xor32(ls);
+    // P^T chunk c = 16 tokens: the lane's s[c/2][8*(c%2) .. +7]
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 4; ++c) {
+        bf16x8_t pb;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)s[c >> 1][(c & 1) * 8 + j];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-        const uint16_t *vrow = &L.vt[(dt * 32 + c32) * VS];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const bf16x4_t lo = *(const bf16x4_t *)&vrow[c * 16 + hf * 4];
-            const bf16x4_t hi = *(const bf16x4_t *)&vrow[c * 16 + 8 + hf * 4];
-            const bf16x8_t va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            st.acc[dt] = ma_mfma32(va, pb[c], st.acc[dt]);
-        }
+        for (int j = 0; j < 8; ++j) pb[j] = (__bf16)s[c >> 1][(c & 1) * 8 + j];
+        pdst[c * 64 + lane] = __builtin_bit_cast(uint4, pb);
     }
 }
 
-// write a row's partial (max in natural-log units, l and acc relative to the exact max)
+// O wave, one tile: O^T = alpha * O^T + V^T P^T.
 template <int D>
-__device__ __forceinline__ void write_partial(const FwdArgs &a, const RowState<D> &st, int bh, int slot, int row,
-                                              int hf) {
+__device__ __forceinline__ void o_tile(const uint16_t *Vt, const uint4 *psrc, const float *asrc, int resc,
+                                       f32x16_t *acc, int c32, int hf, int lane) {
+    constexpr int VS = TILE + 8;
     constexpr int NDT = D / 32;
-    const int64_t prow = ((int64_t)bh * (a.nsplit + 1) + slot) * a.R + row;
-    float f = 0.f;
-    if (st.m_true != -INFINITY) f = __builtin_amdgcn_exp2f((st.m_ref - st.m_true) * a.sl2);
-    if (hf == 0) {
-        a.wm[prow] = st.m_true * a.scale;
-        a.wl[prow] = st.l * f;
+    if (resc) {
+        const float a = asrc[c32];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] *= a;
     }
-    float *dst = a.wacc + prow * D;
+    // chunk c+1's P^T and V^T fragments are loaded before chunk c's MFMAs; within a chunk
+    // the D/32 accumulators alternate, so no MFMA waits on the previous one
+    const uint16_t *vrow = &Vt[c32 * VS + hf * 8];
+    bf16x8_t pc = __builtin_bit_cast(bf16x8_t, psrc[lane]);
+    bf16x8_t va[NDT];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int dt = 0; dt < NDT; ++dt) va[dt] = *(const bf16x8_t *)&vrow[dt * 32 * VS];
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4_t v = {st.acc[dt][q4 * 4 + 0] * f, st.acc[dt][q4 * 4 + 1] * f, st.acc[dt][q4 * 4 + 2] * f,
-                               st.acc[dt][q4 * 4 + 3] * f};
-            *(f32x4_t *)&dst[dt * 32 + q4 * 8 + hf * 4] = v;
+    for (int c = 0; c < 4; ++c) {
+        bf16x8_t nv[NDT], np = pc;
+        if (c + 1 < 4) {
+            np = __builtin_bit_cast(bf16x8_t, psrc[(c + 1) * 64 + lane]);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) nv[dt] = *(const bf16x8_t *)&vrow[dt * 32 * VS + (c + 1) * 16];
         }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = ma_mfma32(va[dt], pc, acc[dt]);
+        if (c + 1 < 4) {
+            pc = np;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) va[dt] = nv[dt];
+        }
+    }
 }
 
-enum { SRC_PACKED = 0, SRC_DENSE = 1 };
+// Workgroup index -> (segment, lane bh, row group, split).  Prefix splits first, the
+// current-block workgroups last (they are short, so they fill in behind the splits).
+struct Work {
+    bool cur;
+    int bh, rg, sp;
+};
 
-// grid (max(nsplit,1), B*H, row groups), NT threads.  Split sp covers prefix tokens
-// [sp*split_n, (sp+1)*split_n); split 0 also attends the current block afterwards and
-// writes it as partial slot nsplit.  The prefix tiles of the source kind SRC run through
-// the register prefetch (the next tile's loads are in flight while the current one is
-// computed); with a packed prefix, its 16-bit residual tail and the current block are
-// staged synchronously (a few tiles per call).
+__device__ __forceinline__ Work decode_work(const FwdArgs &a) {
+    Work w;
+    int idx = blockIdx.x;
+    const int npre = a.nsp * a.BH * a.row_groups;
+    w.cur = idx >= npre;
+    if (w.cur) idx -= npre;
+    w.rg = idx % a.row_groups;
+    idx /= a.row_groups;
+    w.bh = idx % a.BH;
+    w.sp = w.cur ? 0 : idx / a.BH;
+    return w;
+}
+
+// Token source of one workgroup of the 16-bit kernel: the 16-bit part of a prefix, or
+// the current block.  Token j of the workgroup's range lives at k + (j - tok0) * sk.
+struct DSrc {
+    const char *k, *v;
+    int sk, sv, dtype, esz, tok0;
+    const uint8_t *mask;  // liveness by absolute token index, or null
+};
+
 template <int D, int SRC>
-__global__ void __launch_bounds__(NT) splitk_fwd_kernel(FwdArgs a) {
-    __shared__ TileLds<D> T;
+__global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
+    __shared__ FwdSmem<D> S;
+    using Shape = StageShape<KLANES, D, SRC == 0 ? ST_PACKED : ST_DENSE>;
     constexpr int NKS = D / 16;
+    constexpr int NDT = D / 32;
 
-    const int sp = blockIdx.x, bh = blockIdx.y;
-    const int b = bh / a.H, h = bh % a.H;
+    const Work wk = decode_work(a);
+    const int bh = wk.bh, b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
-    const int rtile = blockIdx.z * MAX_WAVES + wave;
-    const int row = rtile * 32 + c32;
-    const bool wave_active = rtile < a.row_tiles;
-    const bool row_ok = row < a.R;
-    const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
-
-    bf16x8_t qf[NKS];
-    {
-        const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
-    }
 
     const Lane L = make_lane(a.pre, b, h, bh);
-    const Dense kc = dense_lane(a.kc.ptr, a.kc.s, a.kc.dtype, b, h);
-    const Dense vc = dense_lane(a.vc.ptr, a.vc.s, a.vc.dtype, b, h);
-    const int nq = L.nq, ntot = L.ntot, Tc = a.Tc;
-    const int pstart = sp * a.split_n;
-    const int pend = min(pstart + a.split_n, ntot);
-    const int n_pt = pstart < pend ? (pend - pstart + TILE - 1) / TILE : 0;
-    const bool with_cur = sp == 0;
-    const int n_ct = with_cur ? (Tc + TILE - 1) / TILE : 0;
-    const int total = n_pt + n_ct;
-    const int qpos = a.q_pos0 + t;
-    const int causal = a.causal, c_pos0 = a.c_pos0;
-    const float sl2 = a.sl2;
-
-    const ItemOffsets off = SRC == SRC_PACKED ? packed_offsets<D>(L, tid) : dense_offsets<D>(L.kf_n, L.vf_n, L.esz, tid);
-    const ItemOffsets coff = dense_offsets<D>(kc.sn, vc.sn, kc.esz, tid);
-
-    auto tile_n0 = [&](int i) { return i < n_pt ? pstart + i * TILE : (i - n_pt) * TILE; };
-    // does tile i go through the prefetch block?
-    auto prefetched = [&](int i) {
-        if (i >= n_pt) return SRC == SRC_DENSE;
-        return prefix_tile_kind(nq, tile_n0(i), pend) == (SRC == SRC_PACKED ? TK_PACKED : TK_DENSE);
-    };
-    using PF = typename std::conditional<SRC == SRC_PACKED, PfPacked, PfDense>::type;
-    auto load = [&](int i, PF &pf) {
-        const int n0 = tile_n0(i);
-        if constexpr (SRC == SRC_PACKED) {
-            load_packed<D, true>(pf, L, off, n0, pend, tid);
+    // token range of this workgroup
+    int n_beg, n_end;
+    if (wk.cur) {
+        n_beg = 0;
+        n_end = a.Tc;
+    } else {
+        n_beg = a.tok_beg + wk.sp * a.split_n;
+        n_end = min(n_beg + a.split_n, a.tok_end);
+        if (n_end < n_beg) n_end = n_beg;
+    }
+    const int nt = (n_end - n_beg + TILE - 1) / TILE;
+    const int slot = wk.cur ? a.nsplit : a.slot0 + wk.sp;
+    DSrc ds;
+    if constexpr (SRC == 1) {
+        if (wk.cur) {
+            const Dense kc = dense_lane(a.kc.ptr, a.kc.s, a.kc.dtype, b, h);
+            const Dense vc = dense_lane(a.vc.ptr, a.vc.s, a.vc.dtype, b, h);
+            ds = DSrc{kc.base, vc.base, kc.sn, vc.sn, kc.dtype, kc.esz, 0, nullptr};
         } else {
-            if (i < n_pt) {
-                const int64_t tb = (int64_t)(n0 - nq);
-                load_dense<D, true>(pf, L.kf + tb * L.kf_n * L.esz, L.vf + tb * L.vf_n * L.esz, L.kf_n, L.vf_n,
-                                    L.fdtype, L.esz, off, &L, n0, pend, tid);
-            } else {
-                load_dense<D, true>(pf, kc.base + (int64_t)n0 * kc.sn * kc.esz, vc.base + (int64_t)n0 * vc.sn * vc.esz,
-                                    kc.sn, vc.sn, kc.dtype, kc.esz, coff, nullptr, n0, Tc, tid);
+            ds = DSrc{L.kf, L.vf, L.kf_n, L.vf_n, L.fdtype, L.esz, L.nq, L.mask};
+        }
+    }
+
+    // roles
+    const int nS = min(MAXS, a.row_tiles - wk.rg * MAXS);
+    const bool is_s = wave < nS;
+    const bool is_o = wave >= 8 && wave - 8 < nS;
+    const int rw = is_o ? wave - 8 : wave;          // row tile within the group
+    const int rtile = wk.rg * MAXS + rw;
+    const int row = rtile * 32 + c32;
+    const bool row_ok = row < a.R;
+    // staging lanes: waves 7..15 (the O waves and two staging-only waves); the S waves keep
+    // their registers for two tiles of S^T and the Q fragments
+    const int st_lane = wave >= 7 ? tid - 7 * 64 : -1;
+    const bool is_k = st_lane >= 0 && st_lane < KLANES;
+    const bool is_v = st_lane >= KLANES;
+    const int kl = st_lane, vl = st_lane - KLANES;
+
+    auto tile_n0 = [&](int i) { return n_beg + i * TILE; };
+    auto live = [&](int j) {
+        if constexpr (SRC == 0) {
+            return lane_live(L, j, n_end);
+        } else {
+            bool ok = j < n_end;
+            if (ds.mask) ok = ok && ds.mask[min(j, L.ntot - 1)] != 0;
+            return ok;
+        }
+    };
+
+    StageRegs<Shape::NW> pr;
+    pr.flags = 0;
+    // K lanes: global loads of tile i into pr; the dequant / copy into a K buffer
+    auto load_k = [&](int i) {
+        const int n0 = tile_n0(i);
+        pr.flags = (kl < TILE && live(n0 + kl)) ? 256u : 0u;
+        if constexpr (SRC == 0) {
+            if (kl < Shape::NK) load_k_packed<D>(pr.w, L, kl, n0, n_end);
+        } else {
+            const char *base = ds.k + (int64_t)(n0 - ds.tok0) * ds.sk * ds.esz;
+#pragma unroll
+            for (int r = 0; r < Shape::KPL; ++r) {
+                const int u = kl + r * KLANES;
+                if (u < Shape::NK) load_k_dense<D>(&pr.w[4 * r], base, ds.sk, ds.dtype, ds.esz, u, n_end - n0);
+            }
+        }
+    };
+    auto store_k = [&](uint16_t *Ks, uint64_t &km) {
+        if constexpr (SRC == 0) {
+            if (kl < Shape::NK) store_k_packed<D>(Ks, pr.w, kl);
+        } else {
+#pragma unroll
+            for (int r = 0; r < Shape::KPL; ++r) {
+                const int u = kl + r * KLANES;
+                if (u < Shape::NK) store_k_dense<D>(Ks, &pr.w[4 * r], u);
+            }
+        }
+        if (kl < TILE) {
+            const uint64_t m = __ballot((pr.flags & 256u) != 0);
+            if (kl == 0) km = m;
+        }
+    };
+    // V lanes: global loads of tile i into pr; the dequant / copy into a V buffer
+    auto load_v = [&](int i) {
+        const int n0 = tile_n0(i);
+        if constexpr (SRC == 0) {
+            if (vl < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vl, n0, n_end);
+        } else {
+            const char *base = ds.v + (int64_t)(n0 - ds.tok0) * ds.sv * ds.esz;
+#pragma unroll
+            for (int r = 0; r < Shape::VPL; ++r) {
+                const int u = vl + r * KLANES;
+                if (u < Shape::NV) {
+                    const int tp = u % (TILE / 2);
+                    load_v_dense<D>(&pr.w[8 * r], base, ds.sv, ds.dtype, ds.esz, u, live(n0 + 2 * tp),
+                                    live(n0 + 2 * tp + 1), n_end - n0);
+                }
+            }
+        }
+    };
+    auto store_v = [&](uint16_t *Vt) {
+        if constexpr (SRC == 0) {
+            if (vl < Shape::NV) store_v_packed<D>(Vt, pr.w, vl);
+        } else {
+#pragma unroll
+            for (int r = 0; r < Shape::VPL; ++r) {
+                const int u = vl + r * KLANES;
+                if (u < Shape::NV) store_v_dense<D>(Vt, &pr.w[8 * r], u);
             }
         }
     };
 
-    RowState<D> st;
-    row_reset(st);
-    PF pf;
-    if (total > 0 && prefetched(0)) load(0, pf);
-    for (int i = 0; i < total; ++i) {
-        const bool cur = i >= n_pt;
-        const int n0 = tile_n0(i);
-        const int end = cur ? Tc : pend;
-        __syncthreads();
-        if (prefetched(i)) {
-            if constexpr (SRC == SRC_PACKED) store_packed<D, true>(T, pf, tid);
-            else store_dense<D, true>(T, pf, tid);
-            store_okmask(T.okmask, pf, tid);
-        } else if (cur) {
-            PfDense tmp;
-            load_dense<D, true>(tmp, kc.base + (int64_t)n0 * kc.sn * kc.esz, vc.base + (int64_t)n0 * vc.sn * vc.esz,
-                                kc.sn, vc.sn, kc.dtype, kc.esz, coff, nullptr, n0, Tc, tid);
-            store_dense<D, true>(T, tmp, tid);
-            store_okmask(T.okmask, tmp, tid);
-        } else {
-            stage_generic<D, true>(T, L, n0, end, tid);
+    const int qpos = a.q_pos0 + (row_ok ? row % a.T : 0);
+    const bool causal = wk.cur && a.causal > 0;
+
+    // The two branches run separate loops (wave-uniform) with the same barrier count, so
+    // the S state (Q fragments, staging registers) and the O state (accumulators, PV
+    // operands) never share registers.
+    if (wave < 7) {
+        // ---- S waves
+        bf16x8_t qf[NKS];
+        float m_ref = -INFINITY, m_true = -INFINITY, l = 0.f;
+        if (is_s) {
+            const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
+            const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
+        }
+        __syncthreads();  // prologue staging done
+        // Iteration it: the S waves issue S^T of tile it+1 (K is staged two tiles ahead)
+        // and, while those MFMAs run, do the softmax of tile it.  Tile masks travel with S^T.
+        f32x16_t sa[2], sb[2];
+        uint64_t ma = 0, mb = 0;
+        if (is_s && nt > 0) {
+            s_qk<D>(S.kt[0].k, qf, c32, hf, sa);
+            ma = S.kmask[0];
+        }
+        __syncthreads();  // K buffer 0 is read: the first iteration stages tile 2 into it
+        auto step = [&](int it, f32x16_t *sc, uint64_t mc, f32x16_t *sn, uint64_t &mn) {
+            const int cb = it & 1;
+            if (is_s && it + 1 < nt) {
+                s_qk<D>(S.kt[cb ^ 1].k, qf, c32, hf, sn);
+                mn = S.kmask[cb ^ 1];
+            }
+            if (is_s && it < nt) {
+                const int n0 = tile_n0(it);
+                const int lim = causal ? (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4 : TILE;
+                const bool need_mask = causal || mc != ~0ull;
+                s_softmax<D>(sc, mc, m_ref, m_true, l, c32, hf, lane, need_mask, lim, a.sl2, &S.p[cb][rw][0][0],
+                             S.alpha[cb][rw], &S.resc[cb][rw]);
+            }
+            __syncthreads();
+        };
+        int it = 0;
+        for (; it + 1 <= nt; it += 2) {
+            step(it, sa, ma, sb, mb);
+            step(it + 1, sb, mb, sa, ma);
+        }
+        if (it <= nt) step(it, sa, ma, sb, mb);
+        if (is_s && hf == 0) {
+            S.fin[rw][0][c32] = m_ref;
+            S.fin[rw][1][c32] = m_true;
+            S.fin[rw][2][c32] = l;
         }
         __syncthreads();
-        if (i + 1 < total && prefetched(i + 1)) load(i + 1, pf);
-        if (wave_active) {
-            const bool cz = cur && causal > 0;
-            const int lim = cz ? (qpos / causal + 1) * causal - c_pos0 - n0 - hf * 4 : TILE;
-            const bool need_mask = cz || T.okmask != ~0ull;
-            attend_tile<D>(T, qf, st, c32, hf, need_mask, lim, sl2);
+    } else {
+        // ---- O waves (PV one tile behind the S waves) and staging: K lanes stage tile it+2,
+        // V lanes tile it
+        f32x16_t acc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
+        // prologue: K tiles 0 and 1 staged, K tile 2 and V tile 0 in flight
+        if (is_k) {
+            if (nt > 0) {
+                load_k(0);
+                store_k(S.kt[0].k, S.kmask[0]);
+            }
+            if (nt > 1) {
+                load_k(1);
+                store_k(S.kt[1].k, S.kmask[1]);
+            }
+            if (nt > 2) load_k(2);
+        } else if (is_v && nt > 0) {
+            load_v(0);
         }
-        if (i == n_pt - 1) {  // prefix segment done
-            if (wave_active && row_ok) write_partial<D>(a, st, bh, sp, row, hf);
-            row_reset(st);
+        __syncthreads();
+        __syncthreads();  // the S waves have read K tile 0 out of buffer 0
+        for (int it = 0; it <= nt; ++it) {
+            const int cb = it & 1, pb = cb ^ 1;
+            if (is_o && it >= 1)
+                o_tile<D>(S.vt[pb].vt, &S.p[pb][rw][0][0], S.alpha[pb][rw], S.resc[pb][rw], acc, c32, hf, lane);
+            if (is_k && it + 2 < nt) {
+                store_k(S.kt[cb].k, S.kmask[cb]);
+                if (it + 3 < nt) load_k(it + 3);
+            } else if (is_v && it < nt) {
+                store_v(S.vt[cb].vt);
+                if (it + 1 < nt) load_v(it + 1);
+            }
+            __syncthreads();
         }
+        __syncthreads();  // final statistics of the S waves
+        if (is_o && row_ok)
+            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, slot, row, hf);
     }
-    if (with_cur && wave_active && row_ok) write_partial<D>(a, st, bh, a.nsplit, row, hf);
 }
 
-// grid (ceil(R / rows_per_block), B*H), 256 threads; D/4 threads per row, 4 channels
-// each.  First the exact maxima over the splits, then every split's weight is known and
-// the loads of different splits are independent.
+// Pass 2: grid (R, B*H), 128 threads = 8 split lanes x 16 channel octets.  The maximum
+// over the prefix splits first; then split lane sl sums splits sl, sl+8, ... with weights
+// l_s * exp(m_s - M), and the 8 lanes' sums are added in lane order through LDS, so the
+// result does not depend on timing.  Then the current block's partial joins.
+constexpr int CMB_SL = 8;
+
 template <int D>
-__global__ void __launch_bounds__(256) splitk_combine_kernel(const float *wm, const float *wl, const float *wacc,
-                                                             int H, int G, int T, int R, int nsplit, ma_tensor4 out,
-                                                             float *mp_out, float *lp_out, void *op_out) {
-    constexpr int TPR = D / 4;
-    constexpr int RPB = 256 / TPR;
-    const int bh = blockIdx.y, b = bh / H, h = bh % H;
-    const int row = blockIdx.x * RPB + threadIdx.x / TPR;
-    const int d0 = (threadIdx.x % TPR) * 4;
-    if (row >= R) return;
+__global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tensor4 out, float *mp_out, float *lp_out,
+                                                             void *op_out) {
+    constexpr int OCT = D / 8;
+    __shared__ float red[CMB_SL][D];
+    __shared__ float lred[CMB_SL];
+    __shared__ float smax[128 / 64];
+    const int row = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    const int tid = threadIdx.x;
+    const int R = a.R, nsplit = a.nsplit;
     const int64_t base = (int64_t)bh * (nsplit + 1) * R + row;
-    float mp = -INFINITY;
-#pragma unroll 16
-    for (int sp = 0; sp < nsplit; ++sp) mp = fmaxf(mp, wm[base + (int64_t)sp * R]);
-    const float msafe_p = (mp == -INFINITY) ? 0.f : mp;
-    float lp = 0.f;
-    f32x4_t op = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int sp = 0; sp < nsplit; ++sp) {
-        const int64_t pr = base + (int64_t)sp * R;
-        const float w = expf(wm[pr] - msafe_p);
-        lp += wl[pr] * w;
-        op += *(const f32x4_t *)&wacc[pr * D + d0] * w;
+    // M = max over the prefix splits
+    float m = -INFINITY;
+    for (int sp = tid; sp < nsplit; sp += 128) m = fmaxf(m, a.wm[base + (int64_t)sp * R]);
+    m = ma_wave_max(m);
+    if ((tid & 63) == 0) smax[tid >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(smax[0], smax[1]);
+    const float msafe = M == -INFINITY ? 0.f : M;
+    const int sl = tid / OCT, oc = tid % OCT;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    if (sl < CMB_SL) {
+        for (int sp = sl; sp < nsplit; sp += CMB_SL) {
+            const int64_t pr = base + (int64_t)sp * R;
+            const float w = a.wl[pr] * expf(a.wm[pr] - msafe);
+            if (w == 0.f) continue;  // an empty split: its O is never read
+            const float ws = w * a.wsc[pr];
+            typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+            const f16x8_t o = *(const f16x8_t *)&a.wo[pr * D + oc * 8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(ws, (float)o[e], acc[e]);
+            lsum += w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[sl][oc * 8 + e] = acc[e];
+        if (oc == 0) lred[sl] = lsum;
     }
+    __syncthreads();
+    if (tid >= D) return;
+    const int d = tid;
+    float op = 0.f, lp = 0.f;
+#pragma unroll
+    for (int k = 0; k < CMB_SL; ++k) {
+        op += red[k][d];
+        lp += lred[k];
+    }
+    // current block (slot nsplit)
     const int64_t pc = base + (int64_t)nsplit * R;
-    const float mc = wm[pc], lc = wl[pc];
-    const f32x4_t ac = *(const f32x4_t *)&wacc[pc * D + d0];
-    const float m = fmaxf(mp, mc);
-    const float msafe = (m == -INFINITY) ? 0.f : m;
-    const float ea = expf(mp - msafe), eb = expf(mc - msafe);
+    const float mc = a.wm[pc], lc = a.wl[pc];
+    const float oc_d = lc > 0.f ? (float)a.wo[pc * D + d] * a.wsc[pc] : 0.f;
+    const float mm = fmaxf(M, mc);
+    const float ms = (mm == -INFINITY) ? 0.f : mm;
+    const float ea = expf(M - ms), eb = expf(mc - ms);
     const float den = lp * ea + lc * eb;
     const float inv = 1.0f / (den > 0.f ? den : 1.0f);
-    const int g = row / T, t = row % T;
-    const int64_t ob = b * out.s[0] + (int64_t)(h * G + g) * out.s[1] + (int64_t)t * out.s[2] + d0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ma_store_f(out.ptr, ob + e, out.dtype, (op[e] * ea + ac[e] * eb) * inv);
+    const int g = row / a.T, t = row % a.T;
+    const int64_t ob = b * out.s[0] + (int64_t)(h * a.G + g) * out.s[1] + (int64_t)t * out.s[2] + d;
+    ma_store_f(out.ptr, ob, out.dtype, (op * ea + lc * oc_d * eb) * inv);
     if (mp_out) {
-        if (d0 == 0) {
-            mp_out[(int64_t)bh * R + row] = mp;
+        if (d == 0) {
+            mp_out[(int64_t)bh * R + row] = M;
             lp_out[(int64_t)bh * R + row] = lp;
         }
-        const float il = 1.0f / (lp > 0.f ? lp : 1.0f);
-        const int64_t oo = ((int64_t)bh * R + row) * D + d0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ma_store_f(op_out, oo + e, out.dtype, op[e] * il);
+        ma_store_f(op_out, ((int64_t)bh * R + row) * D + d, out.dtype, op * (1.0f / (lp > 0.f ? lp : 1.0f)));
     }
 }
 
@@ -329,22 +554,30 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 int ma_validate_prefix(const ma_prefix *p, int D, const char *who);
 
-extern "C" int64_t ma_splitk_workspace_bytes(int B, int H, int Hq, int T, int D, int n, int split_tokens) {
-    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || D <= 0 || n < 0) return -1;
+// Slots of the partials: ceil(nq / sn) packed splits, ceil(nf / sn) 16-bit splits, then
+// the current block.
+static int slot_count(int nq, int nf, int sn) { return (nq + sn - 1) / sn + (nf + sn - 1) / sn; }
+
+static int row_groups_of(int Hq, int H, int T) {
+    const int row_tiles = ((Hq / H) * T + 31) / 32;
+    return (row_tiles + MAXS - 1) / MAXS;
+}
+
+extern "C" int64_t ma_splitk_workspace_bytes(int B, int H, int Hq, int T, int D, int nq, int nf,
+                                             int split_tokens) {
+    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || D <= 0 || nq < 0 || nf < 0) return -1;
     const int R = (Hq / H) * T;
-    const int row_tiles = (R + 31) / 32;
-    const int row_groups = (row_tiles + MAX_WAVES - 1) / MAX_WAVES;
-    const int sn = choose_split(n, B * H, row_groups, split_tokens);
-    const int nsplit = n ? (n + sn - 1) / sn : 0;
+    const int sn = choose_split(nq + nf, B * H, row_groups_of(Hq, H, T), split_tokens);
+    const int nsplit = slot_count(nq, nf, sn);
     const int64_t rows = (int64_t)B * H * (nsplit + 1) * R;
-    return rows * 4 * 2 + rows * D * 4 + 256;
+    return rows * 4 * 3 + rows * D * 2 + 256;
 }
 
 namespace {
 
 struct Plan {
     FwdArgs fa;
-    int waves, row_groups, D, B;
+    int row_groups, D, B;
 };
 
 int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
@@ -379,11 +612,11 @@ int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int
     const int G = Hq / H;
     const int R = G * T;
     const int row_tiles = (R + 31) / 32;
-    const int row_groups = (row_tiles + MAX_WAVES - 1) / MAX_WAVES;
+    const int row_groups = (row_tiles + MAXS - 1) / MAXS;
     const int n = p->nq + p->nf;
     const int sn = choose_split(n, B * H, row_groups, split_tokens);
-    const int nsplit = n ? (n + sn - 1) / sn : 0;
-    const int64_t need = ma_splitk_workspace_bytes(B, H, Hq, T, D, n, sn);
+    const int nsplit = slot_count(p->nq, p->nf, sn);
+    const int64_t need = ma_splitk_workspace_bytes(B, H, Hq, T, D, p->nq, p->nf, sn);
     if (workspace_bytes < need) {
         ma_set_error("%s: workspace %lld bytes < %lld needed", who, (long long)workspace_bytes, (long long)need);
         return MA_EWORKSPACE;
@@ -391,7 +624,8 @@ int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int
     const int64_t rows = (int64_t)B * H * (nsplit + 1) * R;
     float *wm = (float *)workspace;
     float *wl = wm + rows;
-    float *wacc = (float *)(((uintptr_t)(wl + rows) + 15) & ~(uintptr_t)15);
+    float *wsc = wl + rows;
+    _Float16 *wo = (_Float16 *)(((uintptr_t)(wsc + rows) + 15) & ~(uintptr_t)15);
     FwdArgs &fa = pl.fa;
     fa.q = q;
     fa.pre = prefix_dev(p);
@@ -408,29 +642,47 @@ int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int
     fa.q_pos0 = q_pos0;
     fa.c_pos0 = c_pos0;
     fa.row_tiles = row_tiles;
+    fa.row_groups = row_groups;
+    fa.BH = B * H;
     fa.scale = scale;
     fa.sl2 = scale * MA_LOG2E;
     fa.wm = wm;
     fa.wl = wl;
-    fa.wacc = wacc;
-    pl.waves = row_tiles < MAX_WAVES ? row_tiles : MAX_WAVES;
+    fa.wsc = wsc;
+    fa.wo = wo;
     pl.row_groups = row_groups;
     pl.D = D;
     pl.B = B;
     return MA_OK;
 }
 
-int launch_partial(const Plan &pl, hipStream_t st) {
-    dim3 grid(pl.fa.nsplit > 0 ? pl.fa.nsplit : 1, pl.B * pl.fa.H, pl.row_groups);
-    const bool packed = pl.fa.pre.nq > 0;
-    if (pl.D == 128) {
-        if (packed) hipLaunchKernelGGL((splitk_fwd_kernel<128, SRC_PACKED>), grid, dim3(NT), 0, st, pl.fa);
-        else hipLaunchKernelGGL((splitk_fwd_kernel<128, SRC_DENSE>), grid, dim3(NT), 0, st, pl.fa);
-    } else {
-        if (packed) hipLaunchKernelGGL((splitk_fwd_kernel<64, SRC_PACKED>), grid, dim3(NT), 0, st, pl.fa);
-        else hipLaunchKernelGGL((splitk_fwd_kernel<64, SRC_DENSE>), grid, dim3(NT), 0, st, pl.fa);
+template <int D>
+int launch_partial_d(const Plan &pl, hipStream_t st) {
+    // packed part [0, nq): its own launch; the 16-bit part [nq, n) and the current block
+    // (one workgroup per lane and row group, last) in the other
+    FwdArgs fa = pl.fa;
+    const int nq = fa.pre.nq, nf = fa.pre.nf, sn = fa.split_n;
+    const int units = pl.B * fa.H * pl.row_groups;
+    const int nsq = (nq + sn - 1) / sn, nsf = (nf + sn - 1) / sn;
+    if (nsq) {
+        fa.nsp = nsq;
+        fa.slot0 = 0;
+        fa.tok_beg = 0;
+        fa.tok_end = nq;
+        fa.with_cur = 0;
+        hipLaunchKernelGGL((splitk_fwd_kernel<D, 0>), dim3(nsq * units), dim3(NTH), 0, st, fa);
     }
+    fa.nsp = nsf;
+    fa.slot0 = nsq;
+    fa.tok_beg = nq;
+    fa.tok_end = nq + nf;
+    fa.with_cur = 1;
+    hipLaunchKernelGGL((splitk_fwd_kernel<D, 1>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
     return ma_check_launch("ma_splitk_partial");
+}
+
+int launch_partial(const Plan &pl, hipStream_t st) {
+    return pl.D == 128 ? launch_partial_d<128>(pl, st) : launch_partial_d<64>(pl, st);
 }
 
 int launch_merge(const Plan &pl, ma_tensor4 out, float *mp, float *lp, void *op, hipStream_t st) {
@@ -443,14 +695,11 @@ int launch_merge(const Plan &pl, ma_tensor4 out, float *mp, float *lp, void *op,
         return MA_EINVAL;
     }
     const FwdArgs &fa = pl.fa;
-    const int rpb = 256 / (pl.D / 4);
-    dim3 cgrid((fa.R + rpb - 1) / rpb, pl.B * fa.H);
+    const dim3 cgrid(fa.R, pl.B * fa.H);
     if (pl.D == 128)
-        hipLaunchKernelGGL(splitk_combine_kernel<128>, cgrid, dim3(256), 0, st, fa.wm, fa.wl, fa.wacc, fa.H, fa.G,
-                           fa.T, fa.R, fa.nsplit, out, mp, lp, op);
+        hipLaunchKernelGGL(splitk_combine_kernel<128>, cgrid, dim3(128), 0, st, fa, out, mp, lp, op);
     else
-        hipLaunchKernelGGL(splitk_combine_kernel<64>, cgrid, dim3(256), 0, st, fa.wm, fa.wl, fa.wacc, fa.H, fa.G,
-                           fa.T, fa.R, fa.nsplit, out, mp, lp, op);
+        hipLaunchKernelGGL(splitk_combine_kernel<64>, cgrid, dim3(128), 0, st, fa, out, mp, lp, op);
     return ma_check_launch("ma_splitk_merge");
 }
 
@@ -466,15 +715,15 @@ extern "C" int ma_splitk_partial(ma_tensor4 q, int B, int Hq, int T, int D, cons
     return launch_partial(pl, (hipStream_t)stream);
 }
 
-extern "C" int ma_splitk_merge(int B, int Hq, int T, int D, int H, int n, int split_tokens, ma_tensor4 out,
-                               float *mp, float *lp, void *op, void *workspace, int64_t workspace_bytes,
-                               void *stream) {
-    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || n < 0 || (D != 64 && D != 128) || !workspace ||
-        split_tokens < 0 || split_tokens % TILE) {
+extern "C" int ma_splitk_merge(int B, int Hq, int T, int D, int H, int nq, int nf, int split_tokens,
+                               ma_tensor4 out, float *mp, float *lp, void *op, void *workspace,
+                               int64_t workspace_bytes, void *stream) {
+    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || nq < 0 || nf < 0 || (D != 64 && D != 128) ||
+        !workspace || split_tokens < 0 || split_tokens % TILE) {
         ma_set_error("ma_splitk_merge: bad sizes");
         return MA_EINVAL;
     }
-    const int64_t need = ma_splitk_workspace_bytes(B, H, Hq, T, D, n, split_tokens);
+    const int64_t need = ma_splitk_workspace_bytes(B, H, Hq, T, D, nq, nf, split_tokens);
     if (workspace_bytes < need) {
         ma_set_error("ma_splitk_merge: workspace %lld bytes < %lld needed", (long long)workspace_bytes,
                      (long long)need);
@@ -483,13 +732,14 @@ extern "C" int ma_splitk_merge(int B, int Hq, int T, int D, int H, int n, int sp
     Plan pl;
     const int G = Hq / H, R = G * T;
     const int row_tiles = (R + 31) / 32;
-    const int row_groups = (row_tiles + MAX_WAVES - 1) / MAX_WAVES;
-    const int sn = choose_split(n, B * H, row_groups, split_tokens);
-    const int nsplit = n ? (n + sn - 1) / sn : 0;
+    const int row_groups = (row_tiles + MAXS - 1) / MAXS;
+    const int sn = choose_split(nq + nf, B * H, row_groups, split_tokens);
+    const int nsplit = slot_count(nq, nf, sn);
     const int64_t rows = (int64_t)B * H * (nsplit + 1) * R;
     pl.fa.wm = (float *)workspace;
     pl.fa.wl = pl.fa.wm + rows;
-    pl.fa.wacc = (float *)(((uintptr_t)(pl.fa.wl + rows) + 15) & ~(uintptr_t)15);
+    pl.fa.wsc = pl.fa.wl + rows;
+    pl.fa.wo = (_Float16 *)(((uintptr_t)(pl.fa.wsc + rows) + 15) & ~(uintptr_t)15);
     pl.fa.H = H;
     pl.fa.G = G;
     pl.fa.T = T;

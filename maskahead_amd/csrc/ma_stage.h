@@ -1,0 +1,220 @@
+// LDS tile staging of the pipelined attention kernels: 64 tokens of one (batch, KV head)
+// lane of a prefix, dequantized (packed int4) or converted (16/32-bit) to bf16 and laid
+// out for the MFMA operand reads of v_mfma_f32_32x32x16_bf16:
+//   K tile  Ks[t][d], row stride KS = D + 8 bf16 (68 or 36 dwords, 4 mod 32): a lane's
+//           16-byte fragment K[t][8j..8j+7] -- 8 lanes of a ds_read_b128 phase hit 8
+//           disjoint 4-bank groups.
+//   V tile  Vt[d][c], row stride VS = 64 + 8 bf16 (36 dwords), token t stored at column
+//           vcol(t): inside every 16-token chunk bits 2 and 3 of the token index are
+//           swapped, which is the order in which the probabilities P^T come out of the
+//           S^T accumulator (element i of a 32-token S^T half <-> token 8(i/4) + 4h + i%4
+//           for lane half h), so lane half h reads its 8 k-slots as ONE 16-byte fragment.
+// Dead or out-of-range tokens are staged as zero values (never NaN from stale slots);
+// their keys are masked by the tile's live-token mask instead.
+//
+// Staging is split between "K lanes" and "V lanes" (KL each) so that K and V of a tile
+// can be staged in different pipeline iterations: load_*() issues the global loads of one
+// tile into a per-lane register block, store_*() dequantizes it into LDS.  Items:
+//   packed K  (key group gl, channel pair dp, 16-token half th): 2 x 8 code bytes + the
+//             two channels' f16 scale and zero                          -> 2*D items
+//   packed V  (token pair tp, channel group cg, 16-channel half ch): 2 x 8 code bytes +
+//             the two tokens' f16 scale and zero                        -> 2*D items
+//   16-bit K  (token, 8-channel chunk): 16 bytes                         -> 8*D items
+//   16-bit V  (token pair, 8-channel chunk): 2 x 16 bytes                -> 4*D items
+#pragma once
+
+#include "ma_tile.h"
+
+namespace ma {
+
+template <int D>
+struct KTileL {
+    static constexpr int KS = D + 8;
+    uint16_t k[TILE * KS];
+};
+
+template <int D>
+struct VTileL {
+    static constexpr int VS = TILE + 8;
+    uint16_t vt[D * VS];
+};
+
+// column of token t (0..63) inside a V^T row
+__device__ __forceinline__ int vcol(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
+enum { ST_PACKED = 0, ST_DENSE = 1 };
+
+// staging lanes per role
+template <int KLANES, int D, int SRC>
+struct StageShape {
+    static constexpr int NK = SRC == ST_PACKED ? 2 * D : TILE * D / 8;        // K items per tile
+    static constexpr int NV = SRC == ST_PACKED ? 2 * D : TILE / 2 * D / 8;    // V items per tile
+    static constexpr int KPL = (NK + KLANES - 1) / KLANES;                   // items per K lane
+    static constexpr int VPL = (NV + KLANES - 1) / KLANES;                   // items per V lane
+    static constexpr int NWK = SRC == ST_PACKED ? 6 * KPL : 4 * KPL;
+    static constexpr int NWV = SRC == ST_PACKED ? 6 * VPL : 8 * VPL;
+    static constexpr int NW = NWK > NWV ? NWK : NWV;
+};
+
+template <int NW>
+struct StageRegs {
+    uint32_t w[NW];
+    uint32_t flags;   // K lanes: bit 8 = this lane's token (lane < 64) usable; V lanes: bit 2i/2i+1 = tokens live
+};
+
+// ------------------------------------------------------------------ packed K
+// item u: gl = u / D, th = (u / (D/2)) & 1, dp = u % (D/2)
+template <int D>
+__device__ __forceinline__ void load_k_packed(uint32_t *w, const Lane &L, int u, int n0, int end) {
+    const int dp = u % (D / 2), th = (u / (D / 2)) & 1, gl = u / D;
+    const bool full = n0 + TILE <= end;
+    const bool gok = full || n0 + gl * KGRP < end;
+    const int g = gok ? n0 / KGRP + gl : 0;       // a group past the end reads group 0, then zeroes
+    const uint8_t *r0 = L.kq + (int64_t)g * L.kq_g + (int64_t)(2 * dp) * L.kq_d + th * 8;
+    const uint2 x0 = *(const uint2 *)r0;
+    const uint2 x1 = *(const uint2 *)(r0 + L.kq_d);
+    const int64_t so = (int64_t)g * L.ks_g + 2 * dp;
+    const uint32_t sc = *(const uint32_t *)(L.ks + so), zp = *(const uint32_t *)(L.kz + so);
+    w[0] = gok ? x0.x : 0u;
+    w[1] = gok ? x0.y : 0u;
+    w[2] = gok ? x1.x : 0u;
+    w[3] = gok ? x1.y : 0u;
+    w[4] = gok ? sc : 0u;
+    w[5] = gok ? zp : 0u;
+}
+
+template <int D>
+__device__ __forceinline__ void store_k_packed(uint16_t *Ks, const uint32_t *w, int u) {
+    constexpr int KS = D + 8;
+    const int dp = u % (D / 2), th = (u / (D / 2)) & 1, gl = u / D;
+    const float s0 = ma_f16_to_f32(w[4] & 0xffff), s1 = ma_f16_to_f32(w[4] >> 16);
+    const float z0 = ma_f16_to_f32(w[5] & 0xffff), z1 = ma_f16_to_f32(w[5] >> 16);
+    uint32_t *dst = (uint32_t *)&Ks[(gl * KGRP + th * 16) * KS + 2 * dp];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const uint32_t c0 = (w[t >> 3] >> ((t & 7) * 4)) & 15u;
+        const uint32_t c1 = (w[2 + (t >> 3)] >> ((t & 7) * 4)) & 15u;
+        dst[t * (KS / 2)] = ma_pack_bf16x2(ma_dq(c0, s0, z0), ma_dq(c1, s1, z1));
+    }
+}
+
+// ------------------------------------------------------------------ packed V
+// item u: tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6; tokens 2tp, 2tp+1
+template <int D>
+__device__ __forceinline__ void load_v_packed(uint32_t *w, uint32_t &flags, const Lane &L, int u, int n0, int end) {
+    const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
+    const int j = n0 + 2 * tp;
+    const bool l0 = lane_live(L, j, end), l1 = lane_live(L, j + 1, end);
+    // clamped token indices keep every load valid on partial tiles
+    const int j0 = min(j, L.nq - 1), j1 = min(j + 1, L.nq - 1);
+    const uint8_t *p = L.vq + cg * L.vq_c + ch * 8;
+    const uint2 x0 = *(const uint2 *)(p + (int64_t)j0 * L.vq_n);
+    const uint2 x1 = *(const uint2 *)(p + (int64_t)j1 * L.vq_n);
+    const uint32_t s0 = L.vs[(int64_t)j0 * L.vs_n + cg], z0 = L.vz[(int64_t)j0 * L.vs_n + cg];
+    const uint32_t s1 = L.vs[(int64_t)j1 * L.vs_n + cg], z1 = L.vz[(int64_t)j1 * L.vs_n + cg];
+    w[0] = l0 ? x0.x : 0u;
+    w[1] = l0 ? x0.y : 0u;
+    w[2] = l1 ? x1.x : 0u;
+    w[3] = l1 ? x1.y : 0u;
+    w[4] = (l0 ? s0 : 0u) | ((l1 ? s1 : 0u) << 16);
+    w[5] = (l0 ? z0 : 0u) | ((l1 ? z1 : 0u) << 16);
+    flags = (l0 ? 1u : 0u) | (l1 ? 2u : 0u);
+}
+
+template <int D>
+__device__ __forceinline__ void store_v_packed(uint16_t *Vt, const uint32_t *w, int u) {
+    constexpr int VS = TILE + 8;
+    const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
+    const float s0 = ma_f16_to_f32(w[4] & 0xffff), s1 = ma_f16_to_f32(w[4] >> 16);
+    const float z0 = ma_f16_to_f32(w[5] & 0xffff), z1 = ma_f16_to_f32(w[5] >> 16);
+    uint32_t *dst = (uint32_t *)&Vt[(cg * VGRP + ch * 16) * VS + vcol(2 * tp)];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const uint32_t c0 = (w[c >> 3] >> ((c & 7) * 4)) & 15u;
+        const uint32_t c1 = (w[2 + (c >> 3)] >> ((c & 7) * 4)) & 15u;
+        dst[c * (VS / 2)] = ma_pack_bf16x2(ma_dq(c0, s0, z0), ma_dq(c1, s1, z1));
+    }
+}
+
+// ------------------------------------------------------------------ 16/32-bit K and V
+// base: byte pointer of token 0 of the tile; sn: elements per token; tokens usable below
+// `valid` (relative); dead tokens (live == false) are zeroed by the caller for V.
+template <int D>
+__device__ __forceinline__ void load_k_dense(uint32_t *w, const char *base, int sn, int dtype, int esz, int u,
+                                             int valid) {
+    const int t = u / (D / 8), chk = u % (D / 8);
+    const int tc = min(t, valid - 1);
+    bf16x8_t x = load8_bf16(base + ((int64_t)tc * sn + chk * 8) * esz, dtype);
+    if (t >= valid) x = bf16x8_t{};
+    const uint4 q = __builtin_bit_cast(uint4, x);
+    w[0] = q.x;
+    w[1] = q.y;
+    w[2] = q.z;
+    w[3] = q.w;
+}
+
+template <int D>
+__device__ __forceinline__ void store_k_dense(uint16_t *Ks, const uint32_t *w, int u) {
+    constexpr int KS = D + 8;
+    const int t = u / (D / 8), chk = u % (D / 8);
+    *(uint4 *)&Ks[t * KS + chk * 8] = uint4{w[0], w[1], w[2], w[3]};
+}
+
+// item u: tp = u % 32, chk = u / 32
+template <int D>
+__device__ __forceinline__ void load_v_dense(uint32_t *w, const char *base, int sn, int dtype, int esz, int u,
+                                             bool l0, bool l1, int valid) {
+    const int tp = u % (TILE / 2), chk = u / (TILE / 2);
+    const int t0 = min(2 * tp, valid - 1), t1 = min(2 * tp + 1, valid - 1);
+    bf16x8_t x0 = load8_bf16(base + ((int64_t)t0 * sn + chk * 8) * esz, dtype);
+    bf16x8_t x1 = load8_bf16(base + ((int64_t)t1 * sn + chk * 8) * esz, dtype);
+    if (!l0) x0 = bf16x8_t{};
+    if (!l1) x1 = bf16x8_t{};
+    const uint4 a = __builtin_bit_cast(uint4, x0), b = __builtin_bit_cast(uint4, x1);
+    w[0] = a.x;
+    w[1] = a.y;
+    w[2] = a.z;
+    w[3] = a.w;
+    w[4] = b.x;
+    w[5] = b.y;
+    w[6] = b.z;
+    w[7] = b.w;
+}
+
+template <int D>
+__device__ __forceinline__ void store_v_dense(uint16_t *Vt, const uint32_t *w, int u) {
+    constexpr int VS = TILE + 8;
+    const int tp = u % (TILE / 2), chk = u / (TILE / 2);
+    const int col = vcol(2 * tp);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = (w[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        const uint32_t hi = (w[4 + (e >> 1)] >> ((e & 1) * 16)) & 0xffffu;
+        *(uint32_t *)&Vt[(chk * 8 + e) * VS + col] = lo | (hi << 16);
+    }
+}
+
+// ------------------------------------------------------------------ element-wise staging
+// Synchronous staging of any prefix tile (the one straddling the packed / 16-bit
+// boundary, and 16-bit tail tiles of a packed prefix): lanes [0, nl) of the role.
+template <int D>
+__device__ __forceinline__ void stage_k_generic(uint16_t *Ks, const Lane &L, int n0, int end, int lane, int nl) {
+    constexpr int KS = D + 8;
+    for (int it = lane; it < TILE * D; it += nl) {
+        const int t = it / D, d = it % D;
+        const int j = n0 + t;
+        Ks[t * KS + d] = ma_f32_to_bf16(j < end ? lane_key(L, j, d) : 0.f);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_v_generic(uint16_t *Vt, const Lane &L, int n0, int end, int lane, int nl) {
+    constexpr int VS = TILE + 8;
+    for (int it = lane; it < TILE * D; it += nl) {
+        const int t = it % TILE, d = it / TILE;
+        const int j = n0 + t;
+        Vt[d * VS + vcol(t)] = ma_f32_to_bf16(lane_live(L, j, end) ? lane_value(L, j, d) : 0.f);
+    }
+}
+
+}  // namespace ma

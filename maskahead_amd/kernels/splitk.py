@@ -168,7 +168,7 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
         mp = lp = op = None
     lib = N.load()
     n = prefix.n
-    ws_bytes = int(lib.ma_splitk_workspace_bytes(b, hkv, hq, t, d, n, int(split_tokens)))
+    ws_bytes = int(lib.ma_splitk_workspace_bytes(b, hkv, hq, t, d, prefix.nq, prefix.nf, int(split_tokens)))
     if ws_bytes < 0:
         raise ValueError("bad splitk_attention geometry")
     ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
