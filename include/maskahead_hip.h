@@ -95,14 +95,17 @@ int ma_dequant_prefix(const ma_prefix *p, int B, int H, int D, ma_tensor4 k_out,
  * split (multiple of 64; 0 = library default).  The workspace size depends on the packed
  * (nq) and 16-bit (nf) prefix lengths. */
 int64_t ma_splitk_workspace_bytes(int B, int H, int Hq, int T, int D, int nq, int nf, int split_tokens);
-/* The two passes of ma_splitk_attention as separate launches (same arguments and
- * workspace): ma_splitk_partial writes the per-split partials (_sk_fwd, splitk.py:116-190),
- * ma_splitk_merge merges them (_sk_combine, splitk.py:272-318). */
+/* The two passes of ma_splitk_attention as separate calls, with the same arguments and
+ * workspace: ma_splitk_partial writes the per-split partials of the prefix (_sk_fwd,
+ * splitk.py:116-190); ma_splitk_merge attends the current block and merges it with the
+ * partials (the last split of _sk_fwd and _sk_combine, splitk.py:116-190, 272-318). */
 int ma_splitk_partial(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H, ma_tensor4 kc,
                       ma_tensor4 vc, int Tc, int causal_block, int q_pos0, int c_pos0, float scale,
                       int split_tokens, void *workspace, int64_t workspace_bytes, void *stream);
-int ma_splitk_merge(int B, int Hq, int T, int D, int H, int nq, int nf, int split_tokens, ma_tensor4 out,
-                    float *mp, float *lp, void *op, void *workspace, int64_t workspace_bytes, void *stream);
+int ma_splitk_merge(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H, ma_tensor4 kc,
+                    ma_tensor4 vc, int Tc, int causal_block, int q_pos0, int c_pos0, float scale, ma_tensor4 out,
+                    float *mp, float *lp, void *op, int split_tokens, void *workspace, int64_t workspace_bytes,
+                    void *stream);
 int ma_splitk_attention(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
                         ma_tensor4 kc, ma_tensor4 vc, int Tc, int causal_block, int q_pos0,
                         int c_pos0, float scale, ma_tensor4 out, float *mp, float *lp, void *op,

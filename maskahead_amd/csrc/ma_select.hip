@@ -23,11 +23,19 @@ constexpr int NBINS = 2048;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+constexpr int NHC = 4;        // histogram copies (wave w counts into copy w % 4)
+constexpr uint32_t KEY_NEG_INF = 0x007fffffu;   // ma_order_key(-inf); padding keys are 0
+
+constexpr int CAND_MAX = 4096;   // keys of the boundary bin kept in LDS after the first digit
+
 template <int VPT>
 struct SelectSmem {
-    uint32_t hist[NBINS];
+    uint32_t hist[NHC][NBINS];
+    uint32_t cand[CAND_MAX];
+    int ncand;
     int wsum[NW];
-    int found_digit, found_gt;
+    uint32_t kred[2][NW];
+    int found_digit, found_gt, found_cnt;
     int c_eq[VPT][NW], c_sel[VPT][NW];
     int p_eq[VPT + 1], p_sel[VPT + 1];
     int flag;
@@ -52,86 +60,134 @@ __device__ __forceinline__ int block_suffix_incl(int v, SelectSmem<VPT> &S) {
 
 // The k-th largest of the block's keys (1 <= k <= number of keys).  Returns T and sets
 // need = k - count(key > T), the number of keys equal to T that are selected.
+// The digits adapt to the keys' range: above the highest bit in which the largest key and
+// the smallest key above -inf differ, all those keys agree, so the first 11-bit digit
+// starts there (scores that span a few binades then spread over many bins instead of
+// piling into a few, which would serialize the LDS atomics).  Keys at -inf or below only
+// matter when fewer than k keys are above -inf; then T is -inf.
 template <int VPT>
-__device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT> &S, int &need) {
-    const int tid = threadIdx.x;
-    uint32_t prefix = 0u, pmask = 0u;
-    int kk = k;
-#pragma unroll 1
-    for (int p = 0; p < 3; ++p) {
-        const int shift = p == 0 ? 21 : (p == 1 ? 10 : 0);
-        const int nb = p == 2 ? 1024 : 2048;
-        for (int i = tid; i < NBINS; i += NT) S.hist[i] = 0u;
-        __syncthreads();
+__device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT> &S, int &need, int &eq) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // range of the keys above -inf, and how many there are
+    uint32_t kmax = 0u, kmin = 0xffffffffu;
+    int nhi = 0;
 #pragma unroll
-        for (int e = 0; e < VPT; ++e)
-            if ((key[e] & pmask) == prefix) atomicAdd(&S.hist[(key[e] >> shift) & (uint32_t)(nb - 1)], 1u);
+    for (int e = 0; e < VPT; ++e) {
+        const bool hi = key[e] > KEY_NEG_INF;
+        kmax = max(kmax, key[e]);
+        kmin = hi ? min(kmin, key[e]) : kmin;
+        nhi += __popcll(__ballot(hi));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
+    }
+    if (lane == 0) {
+        S.kred[0][wave] = kmax;
+        S.kred[1][wave] = kmin;
+        S.wsum[wave] = nhi;
+    }
+    __syncthreads();
+    int tot_hi = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        kmax = max(kmax, S.kred[0][w]);
+        kmin = min(kmin, S.kred[1][w]);
+        tot_hi += S.wsum[w];
+    }
+    __syncthreads();  // kred / wsum are reused below
+    if (tot_hi < k) {  // fewer than k keys above -inf: T = -inf
+        need = k - tot_hi;
+        eq = -1;        // not counted
+        return KEY_NEG_INF;
+    }
+    const uint32_t diff = kmax ^ kmin;
+    if (diff == 0u) {  // every key above -inf is equal
+        need = k;
+        eq = tot_hi;
+        return kmax;
+    }
+    int hi = 31 - __builtin_clz(diff);            // highest bit that still varies
+    uint32_t pmask = hi == 31 ? 0u : ~((2u << hi) - 1u);
+    uint32_t prefix = kmax & pmask;
+    int kk = k;
+    bool listed = false;      // after the first digit: the boundary bin's keys are in S.cand
+    int ncand = 0;
+#pragma unroll 1
+    while (hi >= 0) {
+        const int w = hi + 1 < 11 ? hi + 1 : 11;
+        const int shift = hi - w + 1;
+        const int nb = 1 << w;
+        for (int i = tid; i < NHC * NBINS; i += NT) (&S.hist[0][0])[i] = 0u;
+        __syncthreads();
+        uint32_t *hist = S.hist[wave % NHC];
+        if (!listed) {
+#pragma unroll
+            for (int e = 0; e < VPT; ++e)
+                if ((key[e] & pmask) == prefix) atomicAdd(&hist[(key[e] >> shift) & (uint32_t)(nb - 1)], 1u);
+        } else {
+            for (int i = tid; i < ncand; i += NT) {
+                const uint32_t x = S.cand[i];
+                if ((x & pmask) == prefix) atomicAdd(&hist[(x >> shift) & (uint32_t)(nb - 1)], 1u);
+            }
+        }
         __syncthreads();
         // thread t owns bins 2t (lower digit) and 2t+1
         const int b0 = 2 * tid;
-        const int c0 = b0 < nb ? (int)S.hist[b0] : 0;
-        const int c1 = b0 + 1 < nb ? (int)S.hist[b0 + 1] : 0;
+        int c0 = 0, c1 = 0;
+        if (b0 < nb) {
+#pragma unroll
+            for (int c = 0; c < NHC; ++c) {
+                c0 += (int)S.hist[c][b0];
+                c1 += (int)S.hist[c][b0 + 1];
+            }
+        }
         const int incl = block_suffix_incl<VPT>(c0 + c1, S);
         const int above = incl - c0 - c1;  // keys with a digit above both of my bins
         if (above < kk && above + c1 >= kk) {
             S.found_digit = b0 + 1;
             S.found_gt = above;
+            S.found_cnt = c1;
         } else if (above + c1 < kk && above + c1 + c0 >= kk) {
             S.found_digit = b0;
             S.found_gt = above + c1;
+            S.found_cnt = c0;
         }
+        if (tid == 0) S.ncand = 0;
         __syncthreads();
         const uint32_t d = (uint32_t)S.found_digit;
+        const int bin_cnt = S.found_cnt;
         kk -= S.found_gt;
         prefix |= d << shift;
         pmask |= (uint32_t)(nb - 1) << shift;
+        hi = shift - 1;
+        if (!listed && hi >= 0 && bin_cnt <= CAND_MAX) {
+            // keep the boundary bin's keys in LDS; later digits read only those
+#pragma unroll
+            for (int e = 0; e < VPT; ++e)
+                if ((key[e] & pmask) == prefix) S.cand[atomicAdd(&S.ncand, 1)] = key[e];
+            __syncthreads();
+            ncand = S.ncand;
+            listed = true;
+        }
+        eq = bin_cnt;
         __syncthreads();  // found_* and wsum are rewritten by the next pass
     }
     need = kk;
     return prefix;
 }
 
-// Select key > T or (key == T and among the first `need` equal keys in index order), and
-// give every selected element its rank in index order.  Writes slot (or -1) per slot e.
+// Output slots of the selected keys (bit e of selbits: slot e of this thread) in index
+// order: counts per (slot, wave), an exclusive scan over them, then each selected key's
+// output slot = keys selected before it.
 template <int VPT, class Emit>
-__device__ void select_and_rank(const uint32_t (&key)[VPT], uint32_t thr, int need, SelectSmem<VPT> &S,
-                                Emit emit) {
+__device__ __forceinline__ void select_emit(uint64_t selbits, SelectSmem<VPT> &S, Emit emit) {
     const int wave = threadIdx.x >> 6, lane = lane_id();
     const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-        const uint64_t be = __ballot(key[e] == thr);
-        if (lane == 0) S.c_eq[e][wave] = __popcll(be);
-    }
-    __syncthreads();
-    // wave 0, lane e: slot e's equal counts -> exclusive prefix over waves (in place) and,
-    // by a wave scan, over slots
-    if (wave == 0) {
-        int tot = 0;
-        if (lane < VPT) {
-            for (int w = 0; w < NW; ++w) {
-                const int c = S.c_eq[lane][w];
-                S.c_eq[lane][w] = tot;
-                tot += c;
-            }
-        }
-        int incl = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
-        }
-        if (lane < VPT) S.p_eq[lane] = incl - tot;
-    }
-    __syncthreads();
-    uint64_t selbits = 0;
-#pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const bool is_eq = key[e] == thr;
-        const int eb = S.p_eq[e] + S.c_eq[e][wave] + __popcll(__ballot(is_eq) & below);
-        const bool sl = key[e] > thr || (is_eq && eb < need);
-        selbits |= (uint64_t)sl << e;
-        const uint64_t bs = __ballot(sl);
+        const uint64_t bs = __ballot((selbits >> e) & 1);
         if (lane == 0) S.c_sel[e][wave] = __popcll(bs);
     }
     __syncthreads();
@@ -161,6 +217,59 @@ __device__ void select_and_rank(const uint32_t (&key)[VPT], uint32_t thr, int ne
     }
 }
 
+// Select key > T or (key == T and among the first `need` equal keys in index order), and
+// give every selected element its rank in index order.  Writes slot (or -1) per slot e.
+template <int VPT, class Emit>
+__device__ void select_and_rank(const uint32_t (&key)[VPT], uint32_t thr, int need, int eq, SelectSmem<VPT> &S,
+                                Emit emit) {
+    const int wave = threadIdx.x >> 6, lane = lane_id();
+    const uint64_t below = (1ull << lane) - 1ull;
+    if (eq == need) {
+        // every key equal to T is selected: no tie ranking needed
+        uint64_t selbits = 0;
+#pragma unroll
+        for (int e = 0; e < VPT; ++e) selbits |= (uint64_t)(key[e] >= thr) << e;
+        select_emit<VPT>(selbits, S, emit);
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+        const uint64_t be = __ballot(key[e] == thr);
+        if (lane == 0) S.c_eq[e][wave] = __popcll(be);
+    }
+    __syncthreads();
+    // wave 0, lane e: slot e's equal counts -> exclusive prefix over waves (in place) and,
+    // by a wave scan, over slots
+    if (wave == 0) {
+        int tot = 0;
+        if (lane < VPT) {
+            for (int w = 0; w < NW; ++w) {
+                const int c = S.c_eq[lane][w];
+                S.c_eq[lane][w] = tot;
+                tot += c;
+            }
+        }
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        if (lane < VPT) S.p_eq[lane] = incl - tot;
+    }
+    __syncthreads();
+    // tie rank of each equal key in index order
+    uint64_t selbits = 0;
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+        const bool is_eq = key[e] == thr;
+        const int eb = S.p_eq[e] + S.c_eq[e][wave] + __popcll(__ballot(is_eq) & below);
+        const bool sl = key[e] > thr || (is_eq && eb < need);
+        selbits |= (uint64_t)sl << e;
+    }
+    select_emit<VPT>(selbits, S, emit);
+}
+
 // ---------------------------------------------------------------- read set
 template <int VPT>
 __global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t rank_stride, const uint8_t *mask,
@@ -185,11 +294,11 @@ __global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t ran
         for (int e = 0; e < CH; ++e)
             key[e0 + e] = (e0 + e) * NT + tid < n ? ma_order_key(mb[e] ? v[e] : -INFINITY) : 0u;
     }
-    int need;
-    const uint32_t thr = radix_kth<VPT>(key, k, S, need);
+    int need, eq;
+    const uint32_t thr = radix_kth<VPT>(key, k, S, need, eq);
     int64_t *out = idx + (int64_t)row * idx_stride;
     float *vout = values ? values + (int64_t)row * k : nullptr;
-    select_and_rank<VPT>(key, thr, need, S, [&](int e, int slot) {
+    select_and_rank<VPT>(key, thr, need, eq, S, [&](int e, int slot) {
         if (slot < k) {
             const int j = e * NT + tid;
             out[slot] = j;
@@ -249,9 +358,9 @@ __global__ void __launch_bounds__(NT) keep_kernel(const PosT *pos, int64_t pos_s
     if (tid == 0 && status) status[row] = S.flag;
     int64_t *out = keep + (int64_t)row * keep_stride;
     if (rest > 0) {
-        int need;
-        const uint32_t thr = radix_kth<VPT>(key, rest, S, need);
-        select_and_rank<VPT>(key, thr, need, S, [&](int e, int slot) {
+        int need, eq;
+        const uint32_t thr = radix_kth<VPT>(key, rest, S, need, eq);
+        select_and_rank<VPT>(key, thr, need, eq, S, [&](int e, int slot) {
             if (slot < rest) out[slot] = e * NT + tid;
         });
     }

@@ -242,6 +242,96 @@ struct DSrc {
     const uint8_t *mask;  // liveness by absolute token index, or null
 };
 
+// The current block of one (lane, row group), for the packed kernel: a few 64-token tiles
+// staged synchronously from the 16-bit current K/V (no pipeline), then S^T, softmax
+// (block-causal mask) and PV as in the main loop; the partial goes to slot nsplit.
+template <int D>
+__device__ __forceinline__ void cur_segment(const FwdArgs &a, const Work &wk, FwdSmem<D> &S) {
+    constexpr int NKS = D / 16;
+    constexpr int NDT = D / 32;
+    const int bh = wk.bh, b = bh / a.H, h = bh % a.H;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
+    const Dense kc = dense_lane(a.kc.ptr, a.kc.s, a.kc.dtype, b, h);
+    const Dense vc = dense_lane(a.vc.ptr, a.vc.s, a.vc.dtype, b, h);
+    const int Tc = a.Tc;
+    const int nt = (Tc + TILE - 1) / TILE;
+    const int nS = min(MAXS, a.row_tiles - wk.rg * MAXS);
+    const bool is_s = wave < nS;
+    const bool is_o = wave >= 8 && wave - 8 < nS;
+    const int rw = is_o ? wave - 8 : wave;
+    const int row = (wk.rg * MAXS + rw) * 32 + c32;
+    const bool row_ok = row < a.R;
+    const int qpos = a.q_pos0 + (row_ok ? row % a.T : 0);
+    const bool causal = a.causal > 0;
+    // S waves and the other waves run separate loops with the same barriers (as in the
+    // main path), so Q fragments and accumulators never share registers
+    if (wave < 7) {
+        bf16x8_t qf[NKS];
+        if (is_s) {
+            const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
+            const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
+        }
+        float m_ref = -INFINITY, m_true = -INFINITY, l = 0.f;
+        for (int i = 0; i < nt; ++i) {
+            const int n0 = i * TILE;
+            __syncthreads();  // tile staged
+            if (is_s) {
+                f32x16_t sv[2];
+                s_qk<D>(S.kt[0].k, qf, c32, hf, sv);
+                const uint64_t okm = S.kmask[0];
+                const int lim = causal ? (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4 : TILE;
+                s_softmax<D>(sv, okm, m_ref, m_true, l, c32, hf, lane, true, lim, a.sl2, &S.p[0][rw][0][0],
+                             S.alpha[0][rw], &S.resc[0][rw]);
+            }
+            __syncthreads();  // P ready
+            __syncthreads();  // PV done, buffers free
+        }
+        if (is_s && hf == 0) {
+            S.fin[rw][0][c32] = m_ref;
+            S.fin[rw][1][c32] = m_true;
+            S.fin[rw][2][c32] = l;
+        }
+        __syncthreads();
+    } else {
+        f32x16_t acc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
+        const int sl = tid - 7 * 64, nsl = NTH - 7 * 64;   // staging lanes
+        for (int i = 0; i < nt; ++i) {
+            const int n0 = i * TILE;
+            const int valid = Tc - n0;
+            uint32_t w[8];
+            const char *kb = kc.base + (int64_t)n0 * kc.sn * kc.esz;
+            for (int u = sl; u < TILE * D / 8; u += nsl) {
+                load_k_dense<D>(w, kb, kc.sn, kc.dtype, kc.esz, u, valid);
+                store_k_dense<D>(S.kt[0].k, w, u);
+            }
+            const char *vb = vc.base + (int64_t)n0 * vc.sn * vc.esz;
+            for (int u = sl; u < TILE / 2 * D / 8; u += nsl) {
+                const int tp = u % (TILE / 2);
+                load_v_dense<D>(w, vb, vc.sn, vc.dtype, vc.esz, u, 2 * tp < valid, 2 * tp + 1 < valid, valid);
+                store_v_dense<D>(S.vt[0].vt, w, u);
+            }
+            if (wave == 7) {
+                const uint64_t m = __ballot(lane < valid);
+                if (lane == 0) S.kmask[0] = m;
+            }
+            __syncthreads();  // tile staged
+            __syncthreads();  // P ready
+            if (is_o) o_tile<D>(S.vt[0].vt, &S.p[0][rw][0][0], S.alpha[0][rw], S.resc[0][rw], acc, c32, hf, lane);
+            __syncthreads();  // PV done
+        }
+        __syncthreads();  // final statistics
+        if (is_o && row_ok)
+            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, a.nsplit, row, hf);
+    }
+}
+
 template <int D, int SRC>
 __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     __shared__ FwdSmem<D> S;
@@ -250,6 +340,12 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     constexpr int NDT = D / 32;
 
     const Work wk = decode_work(a);
+    if constexpr (SRC == 0) {
+        if (wk.cur) {
+            cur_segment<D>(a, wk, S);
+            return;
+        }
+    }
     const int bh = wk.bh, b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
@@ -536,11 +632,13 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
     }
 }
 
+// Tokens per split: about one workgroup per CU (one 133 KB-LDS workgroup fits a CU), with
+// one CU per (lane, row group) left for the current block's workgroups, so every
+// workgroup of the launch runs in the first dispatch wave; never below 256 tokens.
 int choose_split(int n, int BH, int row_groups, int split_tokens) {
     if (split_tokens > 0) return split_tokens;
-    // aim at ~one workgroup per CU for the prefix splits; never below one tile
-    int target = ma_num_cus();
-    int per = target / (BH * row_groups);
+    const int units = BH * row_groups;
+    int per = ma_num_cus() / units - 1;
     if (per < 1) per = 1;
     int sn = (n + per - 1) / per;
     sn = ((sn + TILE - 1) / TILE) * TILE;
@@ -658,26 +756,31 @@ int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int
 
 template <int D>
 int launch_partial_d(const Plan &pl, hipStream_t st) {
-    // packed part [0, nq): its own launch; the 16-bit part [nq, n) and the current block
-    // (one workgroup per lane and row group, last) in the other
+    // packed part [0, nq) and 16-bit part [nq, n) in a launch each; the current block is
+    // attended in the merge
     FwdArgs fa = pl.fa;
     const int nq = fa.pre.nq, nf = fa.pre.nf, sn = fa.split_n;
     const int units = pl.B * fa.H * pl.row_groups;
     const int nsq = (nq + sn - 1) / sn, nsf = (nf + sn - 1) / sn;
+    // the current block's workgroups (last in the grid) ride with the packed launch when
+    // there is no 16-bit part, else with the 16-bit one
+    const bool cur_in_packed = nsq > 0 && nsf == 0;
     if (nsq) {
         fa.nsp = nsq;
         fa.slot0 = 0;
         fa.tok_beg = 0;
         fa.tok_end = nq;
-        fa.with_cur = 0;
-        hipLaunchKernelGGL((splitk_fwd_kernel<D, 0>), dim3(nsq * units), dim3(NTH), 0, st, fa);
+        fa.with_cur = cur_in_packed;
+        hipLaunchKernelGGL((splitk_fwd_kernel<D, 0>), dim3((nsq + fa.with_cur) * units), dim3(NTH), 0, st, fa);
     }
-    fa.nsp = nsf;
-    fa.slot0 = nsq;
-    fa.tok_beg = nq;
-    fa.tok_end = nq + nf;
-    fa.with_cur = 1;
-    hipLaunchKernelGGL((splitk_fwd_kernel<D, 1>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
+    if (!cur_in_packed) {
+        fa.nsp = nsf;
+        fa.slot0 = nsq;
+        fa.tok_beg = nq;
+        fa.tok_end = nq + nf;
+        fa.with_cur = 1;
+        hipLaunchKernelGGL((splitk_fwd_kernel<D, 1>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
+    }
     return ma_check_launch("ma_splitk_partial");
 }
 
@@ -715,38 +818,14 @@ extern "C" int ma_splitk_partial(ma_tensor4 q, int B, int Hq, int T, int D, cons
     return launch_partial(pl, (hipStream_t)stream);
 }
 
-extern "C" int ma_splitk_merge(int B, int Hq, int T, int D, int H, int nq, int nf, int split_tokens,
-                               ma_tensor4 out, float *mp, float *lp, void *op, void *workspace,
+extern "C" int ma_splitk_merge(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H, ma_tensor4 kc,
+                               ma_tensor4 vc, int Tc, int causal_block, int q_pos0, int c_pos0, float scale,
+                               ma_tensor4 out, float *mp, float *lp, void *op, int split_tokens, void *workspace,
                                int64_t workspace_bytes, void *stream) {
-    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || nq < 0 || nf < 0 || (D != 64 && D != 128) ||
-        !workspace || split_tokens < 0 || split_tokens % TILE) {
-        ma_set_error("ma_splitk_merge: bad sizes");
-        return MA_EINVAL;
-    }
-    const int64_t need = ma_splitk_workspace_bytes(B, H, Hq, T, D, nq, nf, split_tokens);
-    if (workspace_bytes < need) {
-        ma_set_error("ma_splitk_merge: workspace %lld bytes < %lld needed", (long long)workspace_bytes,
-                     (long long)need);
-        return MA_EWORKSPACE;
-    }
     Plan pl;
-    const int G = Hq / H, R = G * T;
-    const int row_tiles = (R + 31) / 32;
-    const int row_groups = (row_tiles + MAXS - 1) / MAXS;
-    const int sn = choose_split(nq + nf, B * H, row_groups, split_tokens);
-    const int nsplit = slot_count(nq, nf, sn);
-    const int64_t rows = (int64_t)B * H * (nsplit + 1) * R;
-    pl.fa.wm = (float *)workspace;
-    pl.fa.wl = pl.fa.wm + rows;
-    pl.fa.wsc = pl.fa.wl + rows;
-    pl.fa.wo = (_Float16 *)(((uintptr_t)(pl.fa.wsc + rows) + 15) & ~(uintptr_t)15);
-    pl.fa.H = H;
-    pl.fa.G = G;
-    pl.fa.T = T;
-    pl.fa.R = R;
-    pl.fa.nsplit = nsplit;
-    pl.D = D;
-    pl.B = B;
+    int rc = make_plan(pl, "ma_splitk_merge", q, B, Hq, T, D, p, H, kc, vc, Tc, causal_block, q_pos0, c_pos0, scale,
+                       split_tokens, workspace, workspace_bytes);
+    if (rc) return rc;
     return launch_merge(pl, out, mp, lp, op, (hipStream_t)stream);
 }
 
