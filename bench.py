@@ -32,6 +32,8 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+PASS1_KERNEL = "splitk_fwd_kernel<128, 0>"     # packed-source split-K pass 1 (carries the current block)
+SCORE_KERNEL = "score_kernel<128, 1, 0>"       # value-aware score pass over packed K/V
 
 
 def parse():
@@ -41,8 +43,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="wall-clock budget of the CPU baseline sample (repeated whole steps)")
     ap.add_argument("--eager", action="store_true", help="also time the step without the HIP graph")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="launch a plain 512 MiB device copy three times first, as the calibration "
+                         "kernel of a FETCH_SIZE / WRITE_SIZE counter run")
     return ap.parse_args()
 
 
@@ -57,14 +63,16 @@ def algorithmic(sh):
     gather = k * h * 2 * bkv + k * h * 2 * d * 2
     flops1 = 4 * r * n * d * h
     flops2 = 2 * r * n * d * h
-    return dict(bytes=pass1 + pass2 + scores + gather, flops=flops1 + flops2, pass1_bytes=pass1, pass1_flops=flops1)
+    return dict(bytes=pass1 + pass2 + scores + gather, flops=flops1 + flops2, pass1_bytes=pass1, pass1_flops=flops1,
+                pass2_bytes=pass2 + n * h * 4 * 2, pass2_flops=flops2)
 
 
-def time_graph(fn, steps, warmup):
-    """Capture fn() in a HIP graph, then replay it `warmup` times untimed and `steps`
-    times between two events, all on the current stream (the replay stream).  Every
-    kernel launched by fn uses torch's current stream, which is the capture stream
-    during capture.  Returns ms per replay."""
+def time_graph(fn, steps, warmup, inner=1):
+    """Capture `inner` calls of fn() in one HIP graph, then replay it `warmup` times
+    untimed and `steps` times between two events, all on the current stream (the replay
+    stream).  Every kernel launched by fn uses torch's current stream, which is the
+    capture stream during capture, so the events bracket exactly the replayed kernels.
+    Returns ms per call of fn."""
     side = torch.cuda.Stream()                 # default priority
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -73,7 +81,8 @@ def time_graph(fn, steps, warmup):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for _ in range(inner):
+            fn()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -84,23 +93,44 @@ def time_graph(fn, steps, warmup):
         g.replay()
     e1.record(cur)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps, g
+    return e0.elapsed_time(e1) / (steps * inner), g
 
 
-def cpu_baseline(sh, q, kd, vd, kc, vc, reps):
-    """The reference's CPU torch path for the same step (oracle restatement, float32)."""
+def load_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/traffic_c2_k4v4_n32768.md): the fenced JSON block holds, per kernel,
+    FETCH_SIZE and WRITE_SIZE in KiB per dispatch and the copy-kernel calibration
+    factor of each counter.  None when the summary or the kernel is absent."""
+    f = ROOT / "profiles" / "traffic_c2_k4v4_n32768.md"
+    if not f.exists():
+        return None
+    txt = f.read_text()
+    try:
+        blob = json.loads(txt.split("```json", 1)[1].split("```", 1)[0])
+    except (IndexError, ValueError):
+        return None
+    k = blob.get("kernels", {}).get(kernel)
+    if k is None:
+        return None
+    return int(round(k["fetch_kib"] * 1024 * blob["fetch_factor"] + k["write_kib"] * 1024 * blob["write_factor"]))
+
+
+def cpu_baseline(sh, q, kd, vd, kc, vc, budget_s):
+    """The reference's CPU torch path for the same step (oracle restatement, float32),
+    repeated on whole steps until `budget_s` seconds have passed (at least 3 timed steps,
+    after one warm-up).  Returns (median seconds per step, threads, steps timed)."""
     from oracle import attention as OA
 
     torch.set_num_threads(os.cpu_count() or 1)
     args = (q.float(), kd.float(), vd.float(), kc.float(), vc.float())
-    t0 = time.perf_counter()
     OA.reference_cpu_step(*args, query_indices=range(sh.t), topk=sh.read_k)        # warm-up
     times = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - t_start < budget_s:
         t0 = time.perf_counter()
         OA.reference_cpu_step(*args, query_indices=range(sh.t), topk=sh.read_k)
         times.append(time.perf_counter() - t0)
-    return statistics.median(times), torch.get_num_threads()
+    return statistics.median(times), torch.get_num_threads(), len(times)
 
 
 def main():
@@ -122,6 +152,15 @@ def main():
 
     sh = CONFIGS["c2"]
     dev = torch.device("cuda:0")
+    if a.copy_probe:
+        # calibration kernel for the HBM byte counters: a plain copy of 512 MiB
+        # (536 870 912 B read + 536 870 912 B written per launch)
+        src = torch.ones((512 << 20,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v, kc, vc = layer_inputs(sh, dtype=torch.bfloat16)
     lay = packed_layout(sh.b, sh.hkv, sh.n, sh.d, device=dev)
     quantize_key_groups_into(k.to(dev), lay["kq"], lay["ks"], lay["kz"], bits=4, token_group=32)
@@ -156,7 +195,8 @@ def main():
 
     ms_step, _ = time_graph(step, a.steps, a.warmup)
 
-    # the dominant kernel alone: split-K pass 1 (same arguments, its own graph)
+    # The two large kernels of the step, each alone in its own graph of INNER launches
+    # with the same arguments: split-K pass 1 and the value-aware score pass.
     lib = N.load()
     hq, t, d, hkv = sh.hq, sh.t, sh.d, sh.hkv
     ws_bytes = int(lib.ma_splitk_workspace_bytes(sh.b, hkv, hq, t, d, sh.n, 0, a.split_tokens))
@@ -169,15 +209,14 @@ def main():
                                       a.split_tokens, ws.data_ptr(), ws_bytes,
                                       torch.cuda.current_stream().cuda_stream), "ma_splitk_partial")
 
-    ms_partial, _ = time_graph(partial, a.steps, a.warmup)
+    out0, stats0 = splitk_attention(qg, prefix, kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
 
     def scores_only():
-        _, stats = result["stats_holder"]
-        prefix_scores(qg, prefix, stats, rows, value=True)
+        prefix_scores(qg, prefix, stats0, rows, value=True)
 
-    out0, stats0 = splitk_attention(qg, prefix, kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
-    result["stats_holder"] = (out0, stats0)
-    ms_scores, _ = time_graph(scores_only, a.steps, a.warmup)
+    inner = 10
+    ms_partial, _ = time_graph(partial, a.steps, a.warmup, inner)
+    ms_scores, _ = time_graph(scores_only, a.steps, a.warmup, inner)
 
     ms_eager = None
     if a.eager:
@@ -195,11 +234,29 @@ def main():
     alg = algorithmic(sh)
     t_step = ms_step * 1e-3
     gbs = alg["bytes"] / t_step / 1e9
-    t1 = ms_partial * 1e-3
-    p1_tflops = alg["pass1_flops"] / t1 / 1e12
-    p1_gbs = alg["pass1_bytes"] / t1 / 1e9
+    kernels = {
+        "splitk_partial": dict(kernel=PASS1_KERNEL, ms=ms_partial, flops=alg["pass1_flops"], bytes=alg["pass1_bytes"]),
+        "scores": dict(kernel=SCORE_KERNEL, ms=ms_scores, flops=alg["pass2_flops"], bytes=alg["pass2_bytes"]),
+    }
+    dom_name = max(kernels, key=lambda kk: kernels[kk]["ms"])
+    dom = kernels[dom_name]
+    t_dom = dom["ms"] * 1e-3
+    f_mfma = dom["flops"] / t_dom / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    f_hbm = dom["bytes"] / t_dom / 1e9 / HBM_PEAK_GBS
+    t_mfma_floor = dom["flops"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    t_hbm_floor = dom["bytes"] / (HBM_PEAK_GBS * 1e9)
+    if t_mfma_floor >= t_hbm_floor:
+        roof = {"bound": "mfma", "achieved": round(dom["flops"] / t_dom / 1e12, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(f_mfma, 4)}
+    else:
+        roof = {"bound": "hbm", "achieved": round(dom["bytes"] / t_dom / 1e9, 2), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(f_hbm, 4)}
+    roof["traffic"] = load_traffic(dom["kernel"])
+    roof.update({"kernel": dom["kernel"], "avg_launch_us": round(dom["ms"] * 1e3, 3),
+                 "algorithmic_bytes": dom["bytes"], "algorithmic_flops": dom["flops"],
+                 "hbm_frac": round(f_hbm, 4), "mfma_frac": round(f_mfma, 4)})
     line = {
-        "metric": "µs per layer block-step + achieved HBM GB/s (% roofline), 32k prefix, int4 KV",
+        "metric": "\u00b5s per layer block-step + achieved HBM GB/s (% roofline), 32k prefix, int4 KV",
         "value": round(gbs, 2),
         "unit": "GB/s",
         "us_per_layer_step": round(ms_step * 1e3, 3),
@@ -219,11 +276,8 @@ def main():
                    "prefix": sh.n, "kv": "int4 k4v4 (KG 32, VG 32, f16 scale/zero)",
                    "split_tokens": a.split_tokens or "auto", "graph": True,
                    "algorithmic_bytes": alg["bytes"], "algorithmic_flops": alg["flops"]},
-        "stages_us": {"splitk_partial": round(ms_partial * 1e3, 3), "scores": round(ms_scores * 1e3, 3)},
-        "roofline": {"kernel": "splitk_fwd_kernel<128> (pass 1)", "bound": "mfma",
-                     "achieved": round(p1_tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(p1_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "hbm_gbs": round(p1_gbs, 1), "hbm_frac": round(p1_gbs / HBM_PEAK_GBS, 4)},
+        "stages_us": {kk: round(v["ms"] * 1e3, 3) for kk, v in kernels.items()},
+        "roofline": roof,
     }
     if ms_eager is not None:
         line["eager_us_per_step"] = round(ms_eager * 1e3, 3)
@@ -232,12 +286,14 @@ def main():
 
         kd = OA.dequantize_keys(lay["kq"].cpu(), lay["ks"].cpu(), lay["kz"].cpu()).to(torch.bfloat16)
         vd = OA.dequantize_values(lay["vq"].cpu(), lay["vs"].cpu(), lay["vz"].cpu()).to(torch.bfloat16)
-        sec, cores = cpu_baseline(sh, q, kd, vd, kc, vc, a.cpu_reps)
+        sec, cores, reps = cpu_baseline(sh, q, kd, vd, kc, vc, a.cpu_seconds)
         line["cpu_baseline"] = {"value": round(alg["bytes"] / sec / 1e9, 3), "unit": "GB/s",
                                 "us_per_layer_step": round(sec * 1e6, 1), "cores": cores, "kind": "port",
-                                "sample": f"one full config-2 layer step 0 (prefix {sh.n}, dequantized bf16 K/V, "
-                                          f"float32 torch ops), median of {a.cpu_reps} after 1 warm-up",
-                                "cpu": platform.processor() or platform.machine()}
+                                "sample": f"{reps} whole config-2 step-0 layer steps (prefix {sh.n}, dequantized "
+                                          f"bf16 K/V, float32 torch ops) in ~{a.cpu_seconds:g} s after 1 warm-up; "
+                                          f"median step",
+                                "cpu": platform.processor() or platform.machine(),
+                                "os_cpu_count": os.cpu_count()}
     print(json.dumps(line), flush=True)
 
 
