@@ -8,6 +8,7 @@ kernel is not built for the requested shape, the call raises.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
@@ -86,7 +87,7 @@ def load(path: Path | str | None = None):
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = Path(path) if path is not None else LIB_PATH
+    p = Path(path) if path is not None else Path(os.environ.get("MASKAHEAD_HIP_LIB", LIB_PATH))
     if not p.exists():
         raise KernelUnavailableError(
             f"{p} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "

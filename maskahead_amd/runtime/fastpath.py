@@ -1,0 +1,217 @@
+"""Per-layer orchestration of the read path (the reference session's fast path,
+runtime/session.py:43-75, 430-467, 862-868, 1286-1460).
+
+A session hands every sparse layer's attention to ``FastLayerPath``:
+
+  * step 0 of a block (``step0``, session.py:1403-1454): split-K attention over
+    [live prefix | block] keeping the prefix statistics, the prefix mass and the
+    value-aware score of the selection rows, the read-set top-k with ascending indices
+    and the gather of the selected entries into the layer's compact bf16 buffer;
+  * every later denoising sub-step (``compact_attention``, session.py:1286-1336):
+    attention over [selected entries | block];
+  * look-ahead probes and prefill chunks (``attend``, session.py:1373-1401): block-causal
+    split-K attention with the prefix mass of chosen rows.
+
+Everything runs on the gfx950 kernels of libmaskahead_hip.so.  The sub-step attends
+[compact | block] with split-K directly from the compact buffer and the block's own
+K/V tensors: the reference first copies the block into the compact buffer and calls
+SDPA over it; the result is the same softmax over the same entries.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from .._native import KernelUnavailableError
+from ..kernels.ops import gather_packed_kv
+from ..kernels.select import topk_ascending
+from ..kernels.splitk import Prefix, prefix_scores, splitk_attention
+
+
+def fast_path_supported(config, head_dim: int, device_type: str = "cuda"):
+    """(ok, reason): can this library's kernels serve `config` (session.py:43-75)?
+
+    `config` is the reference's ExperimentConfig (or any object with the same
+    attributes: backend, semantic, async_selector, collect_diagnostics,
+    coverage_diagnostics, compact_format, attn_log_dir, selector, eviction, quant).
+    Beyond the reference's own conditions, the bit widths and group sizes are those
+    this library builds: 4-bit K and V with groups of 32, or 16-bit K and V."""
+    import os
+
+    cfg, sel, ev, q = config, config.selector, config.eviction, config.quant
+    if os.environ.get("BITSIEVE_FAST", "1") == "0" or device_type != "cuda":
+        return False, "disabled or not cuda"
+    if cfg.backend == "torch" or cfg.semantic not in ("A", "dense"):
+        return False, "backend/semantic"
+    if cfg.async_selector and cfg.semantic == "A" and not ev.enabled and not sel.value_aware:
+        return False, "async selector"
+    if cfg.collect_diagnostics or cfg.coverage_diagnostics or cfg.compact_format != "bf16":
+        return False, "diagnostics/compact format"
+    if cfg.attn_log_dir:
+        return False, "attention recording"
+    if sel.score != "softmax" or sel.domain != "prefix" or sel.mode not in ("all", "middle"):
+        return False, "selector score/domain/mode"
+    if sel.value_joint or sel.value_per_query or sel.value_set != "none" or sel.value_caote:
+        return False, "research selector"
+    if sel.value_aware and sel.value_center != "attn":
+        return False, "value centre"
+    if ev.enabled and (ev.policy in ("greedy_set", "oracle_future", "ema_recent_score")
+                       or ev.diag_path or ev.oracle_record_dir):
+        return False, "research eviction"
+    if not ((q.k_bits == 4 and q.v_bits == 4) or (q.k_bits == 16 and q.v_bits == 16)):
+        return False, "bits"
+    if q.k_bits == 4 and (q.key_token_group != 32 or q.value_channel_group != 32):
+        return False, "group sizes"
+    if getattr(q, "key_mode", "channel") != "channel" or getattr(q, "key_bias", "none") != "none" \
+            or getattr(q, "rotation", "none") != "none":
+        return False, "key transform"
+    return head_dim in (64, 128), "head_dim"
+
+
+def effective_topk(old_cache_len: int, topk: int, topk_percent: float | None = None, topk_floor: int | None = None):
+    """Read budget of a block (config.py:172-183)."""
+    import math
+
+    if old_cache_len <= 0:
+        return 0
+    if topk_percent is not None:
+        return min(old_cache_len, max(topk_floor or 1, int(math.ceil(old_cache_len * topk_percent / 100.0))))
+    return min(old_cache_len, topk)
+
+
+@dataclass
+class CompactLayerState:
+    """One layer's compact buffer (session.py:430-454): [B, Hkv, k + block, D]."""
+    key: torch.Tensor
+    value: torch.Tensor
+    indices: torch.Tensor | None = None
+    selected_k: int = 0
+
+
+@dataclass
+class FastLayerPath:
+    """The fast path of one session over its PackedKVCache.
+
+    cache: the session's PackedKVCache; block_size: tokens per block (the compact
+    buffer's tail); query_indices: the block positions of the selection rows;
+    value_aware / sort_indices: the selector's settings; slot_masks: optional uint8
+    [B, Hkv, length] live masks per layer (0 = dead slot)."""
+
+    cache: object
+    block_size: int
+    query_indices: list = field(default_factory=list)
+    value_aware: bool = True
+    sort_indices: bool = True
+    compute_dtype: torch.dtype = torch.bfloat16
+    slot_masks: dict = field(default_factory=dict)
+    states: dict = field(default_factory=dict)
+    last_mass: dict = field(default_factory=dict)
+    _rows_cache: tuple | None = None
+
+    @property
+    def head_dim(self) -> int:
+        return self.cache.head_dim
+
+    def prefix(self, layer_idx: int) -> Prefix:
+        """session.py:1362-1367."""
+        pre = Prefix.from_view(self.cache.layer_view(layer_idx))
+        pre.mask = self.slot_masks.get(layer_idx)
+        return pre
+
+    def rows(self, positions) -> torch.Tensor:
+        """int32 device tensor of block positions, cached per distinct list (session.py:1369-1376)."""
+        key = tuple(int(p) for p in positions)
+        if self._rows_cache is None or self._rows_cache[0] != key:
+            t = torch.tensor(key, dtype=torch.int32).to(self.cache.device, non_blocking=True)
+            self._rows_cache = (key, t)
+        return self._rows_cache[1]
+
+    def current_only(self, query, current_key, current_value, causal: int = 0, q_pos0: int = 0):
+        """Attention over the block alone (session.py:1394-1401)."""
+        out, _ = splitk_attention(query, Prefix(), current_key, current_value, scaling=self.head_dim ** -0.5,
+                                  causal_block=causal, q_pos0=q_pos0, c_pos0=q_pos0)
+        return out
+
+    def attend(self, layer_idx, query, current_key, current_value, *, causal: int = 0, q_pos0: int = 0,
+               mass_rows=None):
+        """Attention over [live prefix | current], optionally with the prefix mass of
+        mass_rows (session.py:1378-1392): look-ahead probes and prefill chunks."""
+        prefix = self.prefix(layer_idx)
+        if prefix.n == 0:
+            return self.current_only(query, current_key, current_value, causal, q_pos0), None
+        out, stats = splitk_attention(query, prefix, current_key, current_value, scaling=self.head_dim ** -0.5,
+                                      causal_block=causal, q_pos0=q_pos0, c_pos0=q_pos0,
+                                      want_prefix=mass_rows is not None)
+        if mass_rows is None:
+            return out, None
+        rows = mass_rows if isinstance(mass_rows, torch.Tensor) else self.rows(mass_rows)
+        mass, _ = prefix_scores(query, prefix, stats, rows, value=False, scaling=self.head_dim ** -0.5)
+        return out, mass
+
+    def ensure_state(self, layer_idx: int, selected_k: int) -> CompactLayerState:
+        """session.py:438-454."""
+        state = self.states.get(layer_idx)
+        capacity = max(1, selected_k) + self.block_size
+        if state is not None and state.key.shape[2] >= capacity:
+            return state
+        shape = (self.cache.batch_size, self.cache.num_kv_heads, capacity, self.head_dim)
+        state = CompactLayerState(key=torch.empty(shape, device=self.cache.device, dtype=self.compute_dtype),
+                                  value=torch.empty(shape, device=self.cache.device, dtype=self.compute_dtype))
+        self.states[layer_idx] = state
+        return state
+
+    def step0(self, layer_idx, query, current_key, current_value, *, select: bool, topk: int,
+              want_mass: bool = False):
+        """Step 0 of a block (session.py:1403-1454): attention over the live prefix and,
+        when `select`, the block's read set of `topk` entries per KV head ranked by mass
+        (or mass * ||v - c|| when value_aware), gathered into the compact buffer.  The
+        prefix mass is kept in last_mass[layer_idx] when want_mass (eviction input)."""
+        need_sel = select and bool(self.query_indices)
+        need_mass = want_mass and bool(self.query_indices)
+        prefix = self.prefix(layer_idx)
+        if prefix.n == 0:
+            return self.current_only(query, current_key, current_value, 0, 0)
+        scale = self.head_dim ** -0.5
+        out, stats = splitk_attention(query, prefix, current_key, current_value, scaling=scale,
+                                      want_prefix=need_sel or need_mass)
+        if not (need_sel or need_mass):
+            return out
+        rows = self.rows(self.query_indices)
+        value = need_sel and self.value_aware
+        mass, score = prefix_scores(query, prefix, stats, rows, value=value, scaling=scale)
+        if need_mass:
+            self.last_mass[layer_idx] = mass
+        if need_sel:
+            k = min(int(topk), prefix.n)
+            if k <= 0:
+                raise ValueError("the read budget must be positive")
+            state = self.ensure_state(layer_idx, k)
+            rank = score if value else mass
+            if not self.sort_indices:
+                raise KernelUnavailableError("the HIP read-set select returns ascending indices only "
+                                             "(selector.sort_indices = False is not built)")
+            idx = topk_ascending(rank, k, prefix.mask)
+            gather_packed_kv(self.cache.layer_view(layer_idx), idx, dtype=self.compute_dtype,
+                             out_key=state.key[:, :, :k, :], out_value=state.value[:, :, :k, :])
+            state.indices = idx
+            state.selected_k = k
+        return out
+
+    def compact_attention(self, layer_idx, query, current_key, current_value):
+        """A denoising sub-step: softmax attention over [selected entries | block]
+        (session.py:1286-1336; sdpa_compact, reference.py:403-426)."""
+        state = self.states.get(layer_idx)
+        if state is None or state.selected_k <= 0:
+            raise RuntimeError(f"layer {layer_idx} has no selected cache; finish_step0 was not called or "
+                               "selection failed")
+        k = state.selected_k
+        ncur = current_key.shape[2]
+        if k + ncur > state.key.shape[2]:
+            raise RuntimeError("compact cache buffer capacity exceeded")
+        cd = self.compute_dtype
+        pre = Prefix.dense(state.key[:, :, :k, :], state.value[:, :, :k, :])
+        out, _ = splitk_attention(query.to(cd), pre, current_key.to(cd), current_value.to(cd),
+                                  scaling=self.head_dim ** -0.5)
+        return out.to(query.dtype)

@@ -1,0 +1,94 @@
+"""Host-side logic of the cache and fast-path mirrors (no GPU): quantization settings and
+their validation (config.py:28-86), the append plan and storage layouts of
+PackedKVCache (cache.py:63-189, 385-421), the read budget (config.py:172-183) and the
+fast-path routing conditions (session.py:43-75)."""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from maskahead_amd._native import KernelUnavailableError
+from maskahead_amd.cache import PackedKVCache
+from maskahead_amd.config import QuantizationConfig
+from maskahead_amd.runtime.fastpath import effective_topk, fast_path_supported
+
+
+def test_quantization_validate_messages():
+    with pytest.raises(ValueError, match="k_bits must be 2, 4, or 16; got 3"):
+        QuantizationConfig(k_bits=3).validate()
+    with pytest.raises(ValueError, match="key_token_group must be a positive multiple of 8"):
+        QuantizationConfig(key_token_group=12).validate()
+    with pytest.raises(ValueError, match="head_dim=100 must be divisible"):
+        QuantizationConfig().validate(head_dim=100)
+    QuantizationConfig().validate(head_dim=128)
+    with pytest.raises(KernelUnavailableError):
+        QuantizationConfig(k_bits=2, v_bits=2).require_built()
+    with pytest.raises(KernelUnavailableError):
+        QuantizationConfig(key_mode="token").require_built()
+    QuantizationConfig(k_bits=16, v_bits=16, key_token_group=8).require_built()
+
+
+def test_cache_layouts_and_append_plan_cpu():
+    c = PackedKVCache(num_layers=3, batch_size=2, num_kv_heads=4, head_dim=128, max_tokens=5000,
+                      quant=QuantizationConfig(), device="cpu")
+    assert c.capacity == 1024 and c.residual_capacity == 63
+    assert tuple(c.k_q.shape) == (3, 2, 4, 32, 128, 16) and tuple(c.k_scale.shape) == (3, 2, 4, 32, 128)
+    assert tuple(c.v_q.shape) == (3, 2, 4, 1024, 4, 16) and tuple(c.v_scale.shape) == (3, 2, 4, 1024, 4)
+    assert c.k_scale.dtype == torch.float16 and c.k_fp is None
+    plan = c.begin_append(1000)
+    assert (plan.quantize_from_residual, plan.new_residual) == (960, 40)
+    with pytest.raises(RuntimeError, match="already in progress"):
+        c.begin_append(1)
+    c.abort_append()
+    plan = c.begin_append(1500)                       # grows the storage past 1024
+    assert c.capacity >= 1536 and c.k_q.shape[3] == c.capacity // 32
+    assert (plan.quantize_from_residual, plan.new_residual) == (1440, 60)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        c.stage_layer(0, torch.zeros(2, 4, 3, 128), torch.zeros(2, 4, 3, 128))
+    with pytest.raises(RuntimeError, match="not staged"):
+        c.commit_append()
+    c.abort_append()
+    with pytest.raises(RuntimeError, match="capacity exceeded"):
+        c.begin_append(6000)
+    b = PackedKVCache(num_layers=1, batch_size=1, num_kv_heads=2, head_dim=64, max_tokens=100,
+                      quant=QuantizationConfig(k_bits=16, v_bits=16), device="cpu")
+    assert b.capacity == 100 and tuple(b.k_fp.shape) == (1, 1, 2, 100, 64) and b.k_q is None
+    with pytest.raises(KernelUnavailableError):
+        PackedKVCache(num_layers=1, batch_size=1, num_kv_heads=2, head_dim=64, max_tokens=100,
+                      quant=QuantizationConfig(), device="cpu", backend="torch")
+
+
+def test_effective_topk():
+    assert effective_topk(0, 512) == 0
+    assert effective_topk(300, 512) == 300
+    assert effective_topk(4096, 512) == 512
+    assert effective_topk(4096, 512, topk_percent=10.0) == 410
+    assert effective_topk(50, 512, topk_percent=1.0, topk_floor=16) == 16
+
+
+def _cfg(**over):
+    sel = SimpleNamespace(score="softmax", domain="prefix", mode="all", value_joint=False, value_per_query=False,
+                          value_set="none", value_caote=False, value_aware=True, value_center="attn")
+    ev = SimpleNamespace(enabled=False, policy="lookahead", diag_path=None, oracle_record_dir=None)
+    q = QuantizationConfig()
+    cfg = SimpleNamespace(backend="auto", semantic="A", async_selector=False, collect_diagnostics=False,
+                          coverage_diagnostics=False, compact_format="bf16", attn_log_dir=None,
+                          selector=sel, eviction=ev, quant=q)
+    for k, v in over.items():
+        obj, _, attr = k.rpartition("__")
+        setattr(getattr(cfg, obj) if obj else cfg, attr, v)
+    return cfg
+
+
+def test_fast_path_supported_reasons():
+    assert fast_path_supported(_cfg(), 128) == (True, "head_dim")
+    assert fast_path_supported(_cfg(), 96) == (False, "head_dim")
+    assert fast_path_supported(_cfg(), 128, "cpu")[1] == "disabled or not cuda"
+    assert fast_path_supported(_cfg(backend="torch"), 128)[1] == "backend/semantic"
+    assert fast_path_supported(_cfg(compact_format="requantized"), 128)[1] == "diagnostics/compact format"
+    assert fast_path_supported(_cfg(selector__mode="uniform"), 128)[1] == "selector score/domain/mode"
+    assert fast_path_supported(_cfg(selector__value_center="mean"), 128)[1] == "value centre"
+    assert fast_path_supported(_cfg(quant=QuantizationConfig(k_bits=2, v_bits=2)), 128)[1] == "bits"
+    assert fast_path_supported(_cfg(quant=QuantizationConfig(key_token_group=16)), 128)[1] == "group sizes"
+    assert fast_path_supported(_cfg(quant=QuantizationConfig(k_bits=16, v_bits=16)), 64) == (True, "head_dim")
