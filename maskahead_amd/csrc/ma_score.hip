@@ -2,61 +2,41 @@
 // per prefix entry j of a KV head,
 //   mass[j]  = (1/(G*T2)) * sum over the selection rows r of exp(s_rj - M_p[r]) / L_p[r]
 //   score[j] = mass[j] * || v_j - centre ||          (value-aware ranking)
-// Workgroup = a run of 64-token tiles of one (batch, KV head) lane; up to 8 waves, each
-// owning one or two 32-row tiles of the selection rows with their Q fragments held in
-// registers.  Per tile the keys are staged (dequantized) in LDS as Ks[t][d] and each wave
-// computes S = Q K^T with v_mfma_f32_32x32x16_bf16 (A = Q, B = K^T), so a lane holds ONE
-// token and 16 rows: the sum over rows is in-register plus one cross-half exchange, then
-// one LDS reduction over waves.  The value distance reads V once per entry, dequantized
-// (and rounded to bf16 when the reference would read its unpacked bf16 prefix).
-#include <type_traits>
-
-#include "ma_tile.h"
+//
+// score_kernel: workgroups of 1024 threads (16 waves, one per CU).  A "fast" workgroup
+// takes a run of whole 64-token tiles of the launch's source kind (packed int4, or
+// 16-bit) of one (batch, KV head) lane, software-pipelined with ONE barrier per tile and
+// fixed wave roles:
+//   * S waves 0 .. row_tiles-1: wave w owns selection rows 32w..32w+31, holds their Q
+//     fragments and per-row constants c_r = M_p[r]*log2e + log2(L_p[r]) in registers,
+//     and computes S = Q K^T of tile i with v_mfma_f32_32x32x16_bf16 (A = Q, B = K^T from
+//     LDS; two independent 32-token accumulators): a lane holds ONE token and 16 rows, so
+//     the sum over rows of exp2(s * scale*log2e - c_r) is 16 exp2 in registers plus one
+//     exchange with lane ^ 32.  Per-(row tile, token) sums go to LDS.
+//   * staging waves (the rest), tile i+1 during tile i: K items (8 tokens x 2 channels)
+//     are dequantized into the other LDS K buffer; V items (one token x 16 channels) give
+//     ||v - centre||^2 partials straight from registers, the D/16 items of a token
+//     reduced by lane shuffles; then the loads of tile i+2 are issued, each from a
+//     per-thread offset fixed for the whole run and a wave-uniform tile base.
+//   * wave 15 (a staging wave) finishes tile i-1: sum over row tiles, live mask, mass and
+//     score.
+// "Tail" workgroups take one of the remaining tiles each (the tile that straddles a
+// packed prefix's 16-bit residual, 16-bit tail tiles, a partial last tile, f32 prefixes)
+// and stage it element-wise.  Both share a prologue that builds, once per workgroup, the
+// selection-row tables in LDS (row of every selection row, its query offset and c_r, one
+// load per row) and the value centre (mean of O_p over the selection rows, a fixed-order
+// LDS reduction shared with ma_value_centre).
+#include "ma_stage.h"
 
 using namespace ma;
 
 namespace {
 
-constexpr int MAX_WAVES = NT / 64;
+constexpr int SNT = 1024;
+constexpr int SWAVES = SNT / 64;
+constexpr int MAX_RT = 16;       // row tiles of 32 selection rows
+constexpr int MAX_R2 = 32 * MAX_RT;
 enum { SRC_PACKED = 0, SRC_DENSE = 1 };
-
-// centre[b,h,:] = mean over rows g*T + q_rows[t2] of f32(op): NTH threads as D channels
-// x (NTH/D) row slices, each slice summing its rows in order, then the slices in order --
-// one fixed summation order, shared by the score kernel's prologue and ma_value_centre.
-template <int D, int NTH>
-__device__ __forceinline__ float centre_partial(const void *op, int op_dtype, int bh, int G, int T,
-                                                const int32_t *q_rows, int T2, int tid) {
-    constexpr int SL = NTH / D;
-    const int d = tid % D, sl = tid / D;
-    const int R = G * T, R2 = G * T2;
-    float s = 0.f;
-    // one loop per dtype: no branch around the loads, which can then all be in flight
-    if (op_dtype == MA_F32) {
-        const float *o = (const float *)op;
-#pragma unroll 8
-        for (int rr = sl; rr < R2; rr += SL) {
-            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
-            s += o[((int64_t)bh * R + row) * D + d];
-        }
-    } else {
-        const uint16_t *o = (const uint16_t *)op;
-        const bool bf = op_dtype == MA_BF16;
-#pragma unroll 8
-        for (int rr = sl; rr < R2; rr += SL) {
-            const int row = (rr / T2) * T + min(max(q_rows[rr % T2], 0), T - 1);
-            const uint16_t x = o[((int64_t)bh * R + row) * D + d];
-            s += bf ? ma_bf16_to_f32(x) : ma_f16_to_f32(x);
-        }
-    }
-    return s;
-}
-
-template <int D, int NTH>
-__device__ __forceinline__ float centre_combine(const float *part, int d, int R2) {
-    float t = 0.f;
-    for (int k = 0; k < NTH / D; ++k) t += part[k * D + d];
-    return t / (float)R2;
-}
 
 struct ScoreArgs {
     ma_tensor4 q;
@@ -66,249 +46,547 @@ struct ScoreArgs {
     const void *op;  // prefix-only output [B*H, R, D] (op_dtype): the value centre's source
     int op_dtype;
     float *mass, *score;
-    int H, G, T, T2, R, R2, row_tiles, tiles_per_wg, value, vround;
+    int H, G, T, T2, R, R2, row_tiles, value, vround;
+    int nfast;     // whole tiles of the source kind per lane: tiles [0, nfast)
+    int per;       // tiles per fast workgroup
+    int fast_wgs;  // fast workgroups per lane (blockIdx.x below it); then one tail tile each
     float sl2;
 };
 
-// distance partials of a packed V item: tokens 2tp, 2tp+1, channels cg*32 + ch*16 + 0..15
+// ------------------------------------------------------------------ value centre
+// centre[d] = (1/R2) * sum over rows r < R of cnt[r] * f32(op[bh, r, d]), cnt[r] = how many
+// of the R2 selection rows are row r (the mean of O_p over the selection rows).  SNT
+// threads: thread (slot s, chunk c) sums rows r = s, s + S, ... (ascending, rows with
+// cnt 0 skipped) of channels 8c..8c+7; slots are then summed in groups of 8, then the
+// groups -- one fixed order, shared by score_kernel and centre_kernel.
 template <int D>
-__device__ __forceinline__ void dist_packed(float (*dpart)[D / 16], const PfPacked &pf, const float *cen, int u,
-                                            bool vround) {
-    const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
-    const float s0 = ma_f16_to_f32(pf.w[4] & 0xffff), s1 = ma_f16_to_f32(pf.w[4] >> 16);
-    const float z0 = ma_f16_to_f32(pf.w[5] & 0xffff), z1 = ma_f16_to_f32(pf.w[5] >> 16);
-    float a0 = 0.f, a1 = 0.f;
+struct CentreSmem {
+    static constexpr int CH = D / 8, S = SNT / CH, QG = SNT / D;
+    float part[S][D];
+    float part2[QG][D];
+};
+
+// the row of selection row rr: (rr / T2) * T + clamp(q_rows[rr % T2], 0, T - 1)
+__device__ __forceinline__ int sel_row(const int32_t *q_rows, int rr, int T2, int T, int *g_out, int *t_out) {
+    const int g = rr / T2;
+    const int t = min(max(q_rows[rr - g * T2], 0), T - 1);
+    *g_out = g;
+    *t_out = t;
+    return g * T + t;
+}
+
+// ------------------------------------------------------------------ staging items
+// Fast tiles are whole 64-token tiles of the launch's source kind.  Every item's global
+// offsets are computed once per thread (32-bit, relative to the tile); per tile only the
+// wave-uniform base pointers move, so the loads take a scalar base + vector offset.
+
+// 8 nibbles of a word as floats, element i = bits 4i..4i+3 (byte masks + cvt_f32_ubyte)
+__device__ __forceinline__ void nib8(uint32_t w, float *f) {
+    const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-        float x0 = ma_dq((pf.w[c >> 3] >> ((c & 7) * 4)) & 15u, s0, z0);
-        float x1 = ma_dq((pf.w[2 + (c >> 3)] >> ((c & 7) * 4)) & 15u, s1, z1);
-        if (vround) {
-            x0 = ma_round_bf16(x0);
-            x1 = ma_round_bf16(x1);
+    for (int b = 0; b < 4; ++b) {
+        f[2 * b] = (float)((lo >> (8 * b)) & 0xffu);
+        f[2 * b + 1] = (float)((hi >> (8 * b)) & 0xffu);
+    }
+}
+
+// K, packed: item u < 4D = (key group gl, 8-token quarter tq, channel pair dp), dp fastest
+// (a wave's LDS writes hit 64 distinct banks).  Words: codes of channel 2dp and 2dp+1
+// (8 tokens each), their f16 scales, their f16 zeros.
+template <int D>
+__device__ __forceinline__ uint2 kp_offsets(const Lane &L, int u) {
+    const int dp = u % (D / 2), tq = (u / (D / 2)) & 3, gl = u / (2 * D);
+    return uint2{(uint32_t)(gl * L.kq_g + 2 * dp * L.kq_d + tq * 4), (uint32_t)(gl * L.ks_g + 2 * dp)};
+}
+
+__device__ __forceinline__ void kp_load(uint32_t *w, const uint8_t *kq, const uint16_t *ks, const uint16_t *kz,
+                                        int kq_d, uint2 o) {
+    w[0] = *(const uint32_t *)(kq + o.x);
+    w[1] = *(const uint32_t *)(kq + o.x + kq_d);
+    w[2] = *(const uint32_t *)(ks + o.y);
+    w[3] = *(const uint32_t *)(kz + o.y);
+}
+
+template <int D>
+__device__ __forceinline__ void kp_store(uint16_t *Ks, const uint32_t *w, int u) {
+    constexpr int KS = D + 8;
+    const int dp = u % (D / 2), tq = (u / (D / 2)) & 3, gl = u / (2 * D);
+    const float s0 = ma_f16_to_f32(w[2] & 0xffff), s1 = ma_f16_to_f32(w[2] >> 16);
+    const float z0 = ma_f16_to_f32(w[3] & 0xffff), z1 = ma_f16_to_f32(w[3] >> 16);
+    float c0[8], c1[8];
+    nib8(w[0], c0);
+    nib8(w[1], c1);
+    uint32_t *dst = (uint32_t *)&Ks[(gl * KGRP + tq * 8) * KS + 2 * dp];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+        dst[t * (KS / 2)] = ma_pack_bf16x2(__builtin_fmaf(c0[t], s0, z0), __builtin_fmaf(c1[t], s1, z1));
+}
+
+// K, 16-bit: item u < 4D = (token t, 16-channel chunk); words: 32 raw bytes.
+template <int D>
+__device__ __forceinline__ uint32_t kd_offset(const Lane &L, int u) {
+    const int t = u / (D / 16), chk = u % (D / 16);
+    return (uint32_t)((t * L.kf_n + chk * 16) * 2);
+}
+
+__device__ __forceinline__ void d32_load(uint32_t *w, const char *base, uint32_t o) {
+    const uint4 *p = (const uint4 *)(base + o);
+    const uint4 a = p[0], b = p[1];
+    w[0] = a.x;
+    w[1] = a.y;
+    w[2] = a.z;
+    w[3] = a.w;
+    w[4] = b.x;
+    w[5] = b.y;
+    w[6] = b.z;
+    w[7] = b.w;
+}
+
+template <int D>
+__device__ __forceinline__ void kd_store(uint16_t *Ks, const uint32_t *w, int u, int dtype) {
+    constexpr int KS = D + 8;
+    const int t = u / (D / 16), chk = u % (D / 16);
+    uint4 *dst = (uint4 *)&Ks[t * KS + chk * 16];
+    if (dtype == MA_BF16) {
+        dst[0] = uint4{w[0], w[1], w[2], w[3]};
+        dst[1] = uint4{w[4], w[5], w[6], w[7]};
+    } else {  // f16 keys enter the dot as bf16 (splitk.py:139, 152)
+        uint32_t o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            o[e] = ma_pack_bf16x2(ma_f16_to_f32(w[e] & 0xffff), ma_f16_to_f32(w[e] >> 16));
+        dst[0] = uint4{o[0], o[1], o[2], o[3]};
+        dst[1] = uint4{o[4], o[5], o[6], o[7]};
+    }
+}
+
+// V, packed: item u < 4D = (token t, 16-channel half hq of a 32-channel group), hq fastest
+// (the D/16 items of a token are adjacent lanes).  Words: 8 code bytes, f16 scale | zero.
+template <int D>
+__device__ __forceinline__ uint2 vp_offsets(const Lane &L, int u) {
+    const int t = u / (D / 16), hq = u % (D / 16), cg = hq >> 1, ch = hq & 1;
+    return uint2{(uint32_t)(t * L.vq_n + cg * L.vq_c + ch * 8), (uint32_t)(t * L.vs_n + cg)};
+}
+
+__device__ __forceinline__ void vp_load(uint32_t *w, const uint8_t *vq, const uint16_t *vs, const uint16_t *vz,
+                                        uint2 o) {
+    const uint2 x = *(const uint2 *)(vq + o.x);
+    w[0] = x.x;
+    w[1] = x.y;
+    w[2] = (uint32_t)vs[o.y] | ((uint32_t)vz[o.y] << 16);
+}
+
+// squared distance of the item's 16 channels to the centre (cen16: those channels, LDS);
+// VR: the values are rounded to bf16 first (the reference's unpacked bf16 prefix)
+template <bool VR>
+__device__ __forceinline__ float vp_dist(const uint32_t *w, const float *cen16) {
+    const float s = ma_f16_to_f32(w[2] & 0xffff), z = ma_f16_to_f32(w[2] >> 16);
+    float q[16];
+    nib8(w[0], q);
+    nib8(w[1], q + 8);
+    float acc = 0.f;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+        const f32x4_t cc = *(const f32x4_t *)&cen16[c4 * 4];
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+            float x0 = __builtin_fmaf(q[c4 * 4 + e], s, z), x1 = __builtin_fmaf(q[c4 * 4 + e + 1], s, z);
+            if constexpr (VR) {
+                const uint32_t pk = ma_pack_bf16x2(x0, x1);
+                x0 = __uint_as_float(pk << 16);
+                x1 = __uint_as_float(pk & 0xffff0000u);
+            }
+            const float d0 = x0 - cc[e], d1 = x1 - cc[e + 1];
+            acc = __builtin_fmaf(d0, d0, acc);
+            acc = __builtin_fmaf(d1, d1, acc);
         }
-        const float cc = cen[cg * VGRP + ch * 16 + c];
-        a0 = __builtin_fmaf(x0 - cc, x0 - cc, a0);
-        a1 = __builtin_fmaf(x1 - cc, x1 - cc, a1);
     }
-    dpart[2 * tp][cg * 2 + ch] = a0;
-    dpart[2 * tp + 1][cg * 2 + ch] = a1;
+    return acc;
 }
 
-// distance partials of a 16-bit V item: tokens 2tp, 2tp+1, channels chk*8 + 0..7
-// (the loader already rounded them to bf16, which is what a 16-bit prefix holds)
+// V, 16-bit: item u < 4D = (token t, 16-channel chunk); words: 32 raw bytes.
 template <int D>
-__device__ __forceinline__ void dist_dense(float (*dpart)[D / 16], const PfDense &pf, const float *cen, int tid) {
-    const int tp = tid % (TILE / 2), chk = tid / (TILE / 2);
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float x0 = ma_bf16_to_f32((pf.w[8 + (e >> 1)] >> ((e & 1) * 16)) & 0xffffu);
-        const float x1 = ma_bf16_to_f32((pf.w[12 + (e >> 1)] >> ((e & 1) * 16)) & 0xffffu);
-        const float cc = cen[chk * 8 + e];
-        a0 = __builtin_fmaf(x0 - cc, x0 - cc, a0);
-        a1 = __builtin_fmaf(x1 - cc, x1 - cc, a1);
-    }
-    // D/8 chunks fold pairwise into D/16 partial slots
-    atomicAdd(&dpart[2 * tp][chk >> 1], a0);
-    atomicAdd(&dpart[2 * tp + 1][chk >> 1], a1);
+__device__ __forceinline__ uint32_t vd_offset(const Lane &L, int u) {
+    const int t = u / (D / 16), chk = u % (D / 16);
+    return (uint32_t)((t * L.vf_n + chk * 16) * 2);
 }
 
-// Workgroup = `tiles_per_wg` consecutive 64-token tiles of one (batch, KV head) lane;
-// NT threads.  Tiles of the source kind SRC go through the register prefetch; the tile
-// straddling a packed prefix's 16-bit tail is staged synchronously.  The V items of the
-// prefetch feed the value distance directly (no V tile in LDS).
-template <int D, int RPW, int SRC>
-__global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
-    __shared__ TileLds<D> T;
-    __shared__ float red[MAX_WAVES][TILE];
-    __shared__ float cen[D];
-    __shared__ float dpart[TILE][D / 16];
-    constexpr int KS = TileLds<D>::KS;
+__device__ __forceinline__ float vd_dist(const uint32_t *w, const float *cen16, int dtype) {
+    float acc = 0.f;
+    const bool bf = dtype == MA_BF16;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+        const f32x4_t cc = *(const f32x4_t *)&cen16[c4 * 4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c4 * 4 + e;
+            const uint32_t wd = w[c >> 1];
+            // as stored (splitk.py:364-369)
+            const float x = bf ? __uint_as_float((c & 1) ? (wd & 0xffff0000u) : (wd << 16))
+                               : ma_f16_to_f32((uint16_t)(wd >> ((c & 1) * 16)));
+            const float dl = x - cc[e];
+            acc = __builtin_fmaf(dl, dl, acc);
+        }
+    }
+    return acc;
+}
+
+// element-wise V distance of item u (any prefix kind; f32 prefixes keep f32 values)
+template <int D>
+__device__ __forceinline__ float vg_dist(const Lane &L, int u, int n0, int end, const float *cen16, bool vround) {
+    const int t = u / (D / 16), c0 = (u % (D / 16)) * 16;
+    const int j = n0 + t;
+    float acc = 0.f;
+    if (j < end) {
+#pragma unroll 2
+        for (int c = 0; c < 16; ++c) {
+            float x = lane_value(L, j, c0 + c);
+            if (vround && j < L.nq) x = ma_round_bf16(x);
+            const float dl = x - cen16[c];
+            acc = __builtin_fmaf(dl, dl, acc);
+        }
+    }
+    return acc;
+}
+
+// sum over the D/16 adjacent lanes of a token (xor tree: every lane of the group ends
+// with the same value)
+template <int D>
+__device__ __forceinline__ float token_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < D / 16; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+constexpr int MAX_R = 1024;   // query rows of a KV head (G * T)
+
+template <int D>
+struct ScoreSmem {
+    union {
+        KTileL<D> kt[2];
+        CentreSmem<D> cs;
+    } u;
+    float red[2][2 * MAX_RT][TILE / 2];  // per (row tile, 32-token half) unit: its token sums
+    float dist[3][TILE];
+    float cen[D];
+    float crow[MAX_R2];         // per selection row: M_p*log2e + log2(L_p), +inf when unused
+    int rrow[MAX_R2];           // per selection row: its row in [0, R)
+    int qoff[MAX_R2];           // per selection row: element offset of its query from (b, h*G, 0)
+    int cnt[MAX_R];             // per row r < R: how many selection rows it is
+};
+
+// Every wave does both jobs, in lock step: S units (a 32-row tile x a 32-token half of a
+// tile, or both halves when the selection needs more than 8 row tiles) and staging items
+// (thread t stages item t: K items [0, 4D), then V items [4D, 8D)).  HALVES: token halves
+// per S unit.
+template <int D, int SRC, int HALVES>
+__global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
+    __shared__ ScoreSmem<D> sm;
+    constexpr int KS = D + 8;
     constexpr int NKS = D / 16;
-    constexpr int NDP = D / 16;
+    constexpr int NIK = 4 * D;                         // K items per tile
+    constexpr int TPI = D / 16;                        // V items (lanes) per token
+    constexpr int NW = SRC == SRC_PACKED ? 4 : 8;      // staging words per item
+    constexpr int CH = D / 8;                          // 8-channel chunks of a row
 
     const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
-    const bool value = a.value, vround = a.vround;
+    const bool value = a.value;
     const float sl2 = a.sl2;
-
-    if (value) {
-        // centre = mean of O_p over the selection rows, in one fixed order per workgroup
-        float *part = &red[0][0];
-        part[tid] = centre_partial<D, NT>(a.op, a.op_dtype, bh, a.G, a.T, a.q_rows, a.T2, tid);
-        __syncthreads();
-        if (tid < D) cen[tid] = centre_combine<D, NT>(part, tid, a.G * a.T2);
-        __syncthreads();
-    }
-    for (int it = tid; it < MAX_WAVES * TILE; it += NT) red[it / TILE][it % TILE] = 0.f;
-
-    // Q fragments (A operand) and per-row statistics of this wave's row tiles
-    bf16x8_t qf[RPW][NKS];
-    float ml2[RPW][16], il[RPW][16];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        // all loads from clamped, valid indices and issued unconditionally; padding rows
-        // then select zeros (they contribute exp2(s*0 - 0) * 0 = 0)
-        const int rt = wave + r * MAX_WAVES;
-        const int rr = rt * 32 + c32;
-        const bool ok = rt < a.row_tiles && rr < a.R2;
-        const int rrc = ok ? rr : 0;
-        const int g = rrc / a.T2;
-        const int t = min(max(a.q_rows[rrc % a.T2], 0), a.T - 1);  // rows outside the block are clamped
-        const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[r][ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[r][ks] = ok ? qf[r][ks] : bf16x8_t{};
-        int qr[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int ri = rt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
-            qr[i] = a.q_rows[(ri < a.R2 ? ri : 0) % a.T2];
-        }
-        float mpv[16], lpv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int ri = rt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
-            const int ric = ri < a.R2 ? ri : 0;
-            const int rf = (ric / a.T2) * a.T + min(max(qr[i], 0), a.T - 1);
-            mpv[i] = a.mp[(int64_t)bh * a.R + rf];
-            lpv[i] = a.lp[(int64_t)bh * a.R + rf];
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int ri = rt * 32 + (i >> 2) * 8 + hf * 4 + (i & 3);
-            const bool rok = rt < a.row_tiles && ri < a.R2;
-            ml2[r][i] = rok ? mpv[i] * MA_LOG2E : 0.f;
-            il[r][i] = rok ? 1.0f / (lpv[i] > 0.f ? lpv[i] : 1.0f) : 0.f;
-        }
-    }
-    const float inv_r2 = 1.0f / (float)a.R2;
     const int row_tiles = a.row_tiles;
-    float *mass_out = a.mass + (int64_t)bh * (a.pre.nq + a.pre.nf);
-    float *score_out = a.score ? a.score + (int64_t)bh * (a.pre.nq + a.pre.nf) : nullptr;
+    const int units = HALVES == 1 ? 2 * row_tiles : row_tiles;
+    const bool s_wave = wave < units;
+    const int rt = HALVES == 1 ? (wave >> 1) : wave;   // this S unit's row tile
+    const int th0 = HALVES == 1 ? (wave & 1) : 0;      // and token half
+    const int end = a.pre.nq + a.pre.nf;
+    const int R = a.R, R2 = a.R2, T = a.T, T2 = a.T2;
+    const bool fast = (int)blockIdx.x < a.fast_wgs;
+    const int tile0 = fast ? blockIdx.x * a.per : a.nfast + (blockIdx.x - a.fast_wgs);
+    const int ntiles = fast ? min(a.per, a.nfast - tile0) : 1;
+    if (ntiles <= 0 || tile0 * TILE >= end) return;   // uniform over the workgroup
 
-    const Lane L = make_lane(a.pre, b, h, bh);
-    const int nq = L.nq, ntot = L.ntot;
-    const ItemOffsets off = SRC == SRC_PACKED ? packed_offsets<D>(L, tid) : dense_offsets<D>(L.kf_n, L.vf_n, L.esz, tid);
-    const int tile0 = blockIdx.x * a.tiles_per_wg;
-    const int ntiles = min(a.tiles_per_wg, (ntot + TILE - 1) / TILE - tile0);
-    using PF = typename std::conditional<SRC == SRC_PACKED, PfPacked, PfDense>::type;
-    auto prefetched = [&](int i) {
-        return prefix_tile_kind(nq, (tile0 + i) * TILE, ntot) == (SRC == SRC_PACKED ? TK_PACKED : TK_DENSE);
-    };
-    auto load = [&](int i, PF &pf) {
-        const int n0 = (tile0 + i) * TILE;
-        if constexpr (SRC == SRC_PACKED) {
-            load_packed<D, true>(pf, L, off, n0, ntot, tid);
-        } else {
-            const int64_t tb = (int64_t)(n0 - nq);
-            load_dense<D, true>(pf, L.kf + tb * L.kf_n * L.esz, L.vf + tb * L.vf_n * L.esz, L.kf_n, L.vf_n, L.fdtype,
-                                L.esz, off, &L, n0, ntot, tid);
-        }
-    };
-    // an f32 prefix keeps f32 values for the distance (splitk.py:364-369 reads them as
-    // stored); the 16-bit loader rounds to bf16, so such tiles take the exact path
-    const bool exact_v = SRC == SRC_DENSE && L.fdtype == MA_F32;
-    auto dist_generic = [&](int n0) {
-        for (int it = tid; it < TILE * NDP; it += NT) {
-            const int tl = it / NDP, c0 = (it % NDP) * 16;
-            const int j = n0 + tl;
-            float ss = 0.f;
-            if (j < ntot) {
-                for (int c = 0; c < 16; ++c) {
-                    float x = lane_value(L, j, c0 + c);
-                    if (vround) x = ma_round_bf16(x);
-                    const float dl = x - cen[c0 + c];
-                    ss = __builtin_fmaf(dl, dl, ss);
-                }
-            }
-            dpart[tl][it % NDP] = ss;
-        }
-    };
-
-    PF pf;
-    if (ntiles > 0 && prefetched(0)) load(0, pf);
-    for (int i = 0; i < ntiles; ++i) {
-        const int n0 = (tile0 + i) * TILE;
-        const bool pre_i = prefetched(i);
-        __syncthreads();
-        if (pre_i) {
-            if constexpr (SRC == SRC_PACKED) {
-                store_packed<D, false>(T, pf, tid);
-                if (value && tid >= 2 * D && tid < 4 * D) dist_packed<D>(dpart, pf, cen, tid - 2 * D, vround);
-            } else {
-                if (value && !exact_v)
-                    for (int it = tid; it < TILE * NDP; it += NT) dpart[it / NDP][it % NDP] = 0.f;
-                store_dense<D, false>(T, pf, tid);
-            }
-            store_okmask(T.okmask, pf, tid);
-        } else {
-            stage_generic<D, false>(T, L, n0, ntot, tid);
-        }
-        if (value && (!pre_i || exact_v)) dist_generic(n0);
-        __syncthreads();
-        if constexpr (SRC == SRC_DENSE) {
-            // 16-bit V items fold into the zeroed partial slots after the barrier
-            if (value && !exact_v && pre_i && tid < TILE / 2 * D / 8) dist_dense<D>(dpart, pf, cen, tid);
-        }
-        if (i + 1 < ntiles && prefetched(i + 1)) load(i + 1, pf);
-
-        float part[2] = {0.f, 0.f};  // this lane's token in each 32-token sub-tile
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            if (wave + r * MAX_WAVES >= row_tiles) break;
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2) {
-                f32x16_t sv = f32x16_t{};
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    const bf16x8_t kb = *(const bf16x8_t *)&T.k[(t2 * 32 + c32) * KS + ks * 16 + hf * 8];
-                    sv = ma_mfma32(qf[r][ks], kb, sv);
-                }
-                float acc = 0.f;
-#pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    acc = __builtin_fmaf(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], sl2, -ml2[r][e])), il[r][e], acc);
-                part[t2] += acc;
-            }
-        }
-        part[0] = ma_sum_xor32(part[0]);
-        part[1] = ma_sum_xor32(part[1]);
-        if (hf == 0) {
-            red[wave][c32] = part[0];
-            red[wave][32 + c32] = part[1];
-        }
-        __syncthreads();
-        if (tid < TILE) {
-            const int j = n0 + tid;
-            if (j < ntot) {
-                const bool live = (T.okmask >> tid) & 1;
-                float sm = 0.f;
-#pragma unroll
-                for (int w = 0; w < MAX_WAVES; ++w) sm += red[w][tid];
-                const float mass_j = live ? sm * inv_r2 : 0.f;
-                mass_out[j] = mass_j;
-                if (value) {
-                    float ss = 0.f;
-#pragma unroll
-                    for (int c = 0; c < NDP; ++c) ss += dpart[tid][c];
-                    score_out[j] = live ? mass_j * sqrtf(ss) : 0.f;
-                }
-            }
-        }
+    // ---- fast staging state: this thread's item offsets inside a tile, once
+    const int ni = value ? 2 * NIK : NIK;              // staging items per tile
+    const bool has_item = tid < ni;
+    uint32_t w[NW];
+    uint2 off = uint2{0u, 0u};
+    const uint8_t *kq0 = nullptr, *vq0 = nullptr;
+    const uint16_t *ks0 = nullptr, *kz0 = nullptr, *vs0 = nullptr, *vz0 = nullptr;
+    const char *kf0 = nullptr, *vf0 = nullptr;
+    int64_t kq_tile = 0, ks_tile = 0, vq_tile = 0, vs_tile = 0, kf_tile = 0, vf_tile = 0;
+    int kq_d = 0;
+    if (fast) {
+        const Lane L = make_lane(a.pre, b, h, bh);
+        if (tid < NIK) off = SRC == SRC_PACKED ? kp_offsets<D>(L, tid) : uint2{kd_offset<D>(L, tid), 0u};
+        else if (has_item)
+            off = SRC == SRC_PACKED ? vp_offsets<D>(L, tid - NIK) : uint2{vd_offset<D>(L, tid - NIK), 0u};
+        kq0 = L.kq;
+        ks0 = L.ks;
+        kz0 = L.kz;
+        vq0 = L.vq;
+        vs0 = L.vs;
+        vz0 = L.vz;
+        kf0 = L.kf;
+        vf0 = L.vf;
+        kq_d = L.kq_d;
+        kq_tile = (int64_t)(TILE / KGRP) * L.kq_g;     // bytes per tile
+        ks_tile = (int64_t)(TILE / KGRP) * L.ks_g;     // elements per tile
+        vq_tile = (int64_t)TILE * L.vq_n;
+        vs_tile = (int64_t)TILE * L.vs_n;
+        kf_tile = (int64_t)TILE * L.kf_n * 2;
+        vf_tile = (int64_t)TILE * L.vf_n * 2;
     }
+    // this thread's item of tile i of the run into w
+    auto load = [&](int i) {
+        const int64_t ti = tile0 + i;   // whole tiles: packed tile ti starts at key group 2*ti
+        if (tid < NIK) {
+            if constexpr (SRC == SRC_PACKED) kp_load(w, kq0 + ti * kq_tile, ks0 + ti * ks_tile, kz0 + ti * ks_tile, kq_d, off);
+            else d32_load(w, kf0 + ti * kf_tile, off.x);
+        } else if (has_item) {
+            if constexpr (SRC == SRC_PACKED) vp_load(w, vq0 + ti * vq_tile, vs0 + ti * vs_tile, vz0 + ti * vs_tile, off);
+            else d32_load(w, vf0 + ti * vf_tile, off.x);
+        }
+    };
+
+    // ---- prologue: the first tile's loads, then the selection-row tables (one load per
+    // row), then Q and the value centre
+    if (fast) load(0);
+    for (int r = tid; r < MAX_R; r += SNT) sm.cnt[r] = 0;
+    __syncthreads();
+    const int rt_pad = 32 * row_tiles;
+    for (int rr = tid; rr < rt_pad; rr += SNT) {
+        float c = __builtin_inff();
+        int row = 0, qo = -1;
+        if (rr < R2) {
+            int g, t;
+            row = sel_row(a.q_rows, rr, T2, T, &g, &t);
+            qo = g * (int)a.q.s[1] + t * (int)a.q.s[2];
+            atomicAdd(&sm.cnt[row], 1);
+            const float m = a.mp[(int64_t)bh * R + row], l = a.lp[(int64_t)bh * R + row];
+            // exp(s - M) / L == exp2(s*log2e - (M*log2e + log2 L)); rows without a live
+            // prefix entry (L = 0) and padding rows contribute exactly 0
+            if (l > 0.f) c = __builtin_fmaf(m, MA_LOG2E, __log2f(l));
+        }
+        sm.crow[rr] = c;
+        sm.rrow[rr] = row;
+        sm.qoff[rr] = qo;
+    }
+    __syncthreads();
+    bf16x8_t qf[NKS];
+    if (s_wave) {
+        const int qo = sm.qoff[rt * 32 + c32];
+        const int64_t qb = b * a.q.s[0] + (int64_t)h * a.G * a.q.s[1] + (qo < 0 ? 0 : qo);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = qo < 0 ? bf16x8_t{} : qf[ks];
+    }
+
+    // value centre: centre[d] = (1/R2) * sum over rows r of cnt[r] * f32(O_p[r][d]), rows of
+    // a slot in ascending order, then slots in groups of 8, then the groups
+    if (value) {
+        using CS = CentreSmem<D>;
+        const int osl = tid / CH, och = tid % CH;
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+        for (int r = osl; r < R; r += SNT / CH) {
+            const int n = sm.cnt[r];
+            if (n > 0) {
+                const int64_t off_o = ((int64_t)bh * R + r) * D + och * 8;
+                float x[8];
+                if (a.op_dtype == MA_F32) {
+                    const f32x4_t *pp = (const f32x4_t *)((const float *)a.op + off_o);
+                    const f32x4_t x0 = pp[0], x1 = pp[1];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x[e] = x0[e];
+                        x[4 + e] = x1[e];
+                    }
+                } else {
+                    const uint4 v4 = *(const uint4 *)((const uint16_t *)a.op + off_o);
+                    const uint32_t wv[4] = {v4.x, v4.y, v4.z, v4.w};
+                    const bool bf = a.op_dtype == MA_BF16;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint16_t hx = (uint16_t)(wv[e >> 1] >> ((e & 1) * 16));
+                        x[e] = bf ? ma_bf16_to_f32(hx) : ma_f16_to_f32(hx);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] += (float)n * x[e];
+            }
+        }
+        CS &cs = sm.u.cs;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cs.part[osl][och * 8 + e] = acc[e];
+        __syncthreads();
+        {
+            const int d = tid % D, q = tid / D;
+            float t = 0.f;
+#pragma unroll
+            for (int k = 0; k < CS::S / CS::QG; ++k) t += cs.part[q * (CS::S / CS::QG) + k][d];
+            cs.part2[q][d] = t;
+        }
+        __syncthreads();
+        if (tid < D) {
+            float t = 0.f;
+#pragma unroll
+            for (int q = 0; q < CS::QG; ++q) t += cs.part2[q][tid];
+            sm.cen[tid] = t / (float)R2;
+        }
+        __syncthreads();
+    }
+
+    // ---- S unit: tile in K buffer kb into the unit's token sums red[rb]
+    auto s_tile = [&](int kb, int rb) {
+        const uint16_t *Ks = sm.u.kt[kb].k;
+#pragma unroll
+        for (int hh = 0; hh < HALVES; ++hh) {
+            const int th = HALVES == 1 ? th0 : hh;
+            f32x16_t sv = f32x16_t{};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const bf16x8_t kf = *(const bf16x8_t *)&Ks[(th * 32 + c32) * KS + ks * 16 + hf * 8];
+                sv = ma_mfma32(qf[ks], kf, sv);
+            }
+            float acc = 0.f;
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                // rows 8*i4 + 4*hf + 0..3 of the row tile
+                const f32x4_t c4 = *(const f32x4_t *)&sm.crow[rt * 32 + i4 * 8 + hf * 4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i4 * 4 + e], sl2, -c4[e]));
+            }
+            acc = ma_sum_xor32(acc);
+            if (hf == 0) sm.red[rb][rt * 2 + th][c32] = acc;
+        }
+    };
+
+    const float inv_r2 = 1.0f / (float)R2;
+    auto finish = [&](int tile, int rb, int db) {
+        const int j = tile * TILE + lane;
+        if (j < end) {
+            float s = 0.f;
+            const int th = lane >> 5, tl = lane & 31;
+            for (int r = 0; r < row_tiles; ++r) s += sm.red[rb][r * 2 + th][tl];
+            bool live = true;
+            if (a.pre.mask) live = a.pre.mask[(int64_t)bh * end + j] != 0;
+            const float m = live ? s * inv_r2 : 0.f;
+            a.mass[(int64_t)bh * end + j] = m;
+            if (value) a.score[(int64_t)bh * end + j] = live ? m * __builtin_sqrtf(sm.dist[db][lane]) : 0.f;
+        }
+    };
+
+    if (!fast) {
+        // ---- tail workgroup: one tile, staged element-wise by every thread
+        const Lane L = make_lane(a.pre, b, h, bh);
+        const int n0 = tile0 * TILE;
+        uint16_t *Ks = sm.u.kt[0].k;
+#pragma unroll 1
+        for (int it = tid; it < TILE * D; it += SNT) {
+            const int t = it / D, d = it % D;
+            const int j = n0 + t;
+            Ks[t * KS + d] = ma_f32_to_bf16(j < end ? lane_key(L, j, d) : 0.f);
+        }
+        if (value) {
+            // V items (token, 16 channels): one per thread, the D/16 lanes of a token adjacent
+            const int v = tid;
+            float dd = v < NIK ? vg_dist<D>(L, v, n0, end, &sm.cen[(v % TPI) * 16], a.vround) : 0.f;
+            dd = token_sum<D>(dd);
+            if (v < NIK && v % TPI == 0) sm.dist[0][v / TPI] = dd;
+        }
+        __syncthreads();
+        if (s_wave) s_tile(0, 0);
+        __syncthreads();
+        if (wave == SWAVES - 1) finish(tile0, 0, 0);
+        return;
+    }
+
+    // ---- fast workgroup: this thread's item of the tile in w into K buffer kb and
+    // distance buffer db
+    const bool vround = a.vround;
+    const float *cen16 = &sm.cen[(has_item && tid >= NIK ? (tid - NIK) % TPI : 0) * 16];
+    auto stage = [&](int kb, int db) {
+        uint16_t *Ks = sm.u.kt[kb].k;
+        if (tid < NIK) {
+            if constexpr (SRC == SRC_PACKED) kp_store<D>(Ks, w, tid);
+            else kd_store<D>(Ks, w, tid, a.pre.fdtype);
+        } else if (value && tid < NIK + NIK) {
+            float dd = 0.f;
+            if constexpr (SRC == SRC_PACKED) dd = vround ? vp_dist<true>(w, cen16) : vp_dist<false>(w, cen16);
+            else dd = vd_dist(w, cen16, a.pre.fdtype);
+            dd = token_sum<D>(dd);
+            if ((tid - NIK) % TPI == 0) sm.dist[db][(tid - NIK) / TPI] = dd;
+        }
+    };
+
+    stage(0, 0);
+    if (ntiles > 1) load(1);
+    __syncthreads();
+
+    for (int i = 0; i < ntiles; ++i) {
+        if (s_wave) s_tile(i & 1, i & 1);
+        // staging of tile i + 1, then the loads of tile i + 2
+        if (i + 1 < ntiles) {
+            stage((i + 1) & 1, (i + 1) % 3);
+            if (i + 2 < ntiles) load(i + 2);
+        }
+        // tile i - 1 is complete in LDS since the last barrier
+        if (wave == SWAVES - 1 && i > 0) finish(tile0 + i - 1, (i - 1) & 1, (i - 1) % 3);
+        __syncthreads();
+    }
+    if (wave == SWAVES - 1) finish(tile0 + ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) % 3);
 }
 
+// the value centre of prefix_scores alone (same definition and order as score_kernel)
 template <int D>
-__global__ void __launch_bounds__(NT) centre_kernel(const void *op, int op_dtype, int G, int T,
-                                                    const int32_t *q_rows, int T2, float *centre) {
-    __shared__ float part[NT];
+__global__ void __launch_bounds__(SNT) centre_kernel(const void *op, int op_dtype, int G, int T,
+                                                     const int32_t *q_rows, int T2, float *centre) {
+    using CS = CentreSmem<D>;
+    constexpr int CH = D / 8;
+    __shared__ CS cs;
+    __shared__ float cen[D];
+    __shared__ int cnt[MAX_R];
     const int bh = blockIdx.x, tid = threadIdx.x;
-    part[tid] = centre_partial<D, NT>(op, op_dtype, bh, G, T, q_rows, T2, tid);
+    const int R = G * T, R2 = G * T2;
+    for (int r = tid; r < R; r += SNT) cnt[r] = 0;
     __syncthreads();
-    if (tid < D) centre[(int64_t)bh * D + tid] = centre_combine<D, NT>(part, tid, G * T2);
+    for (int rr = tid; rr < R2; rr += SNT) {
+        int g, t;
+        atomicAdd(&cnt[sel_row(q_rows, rr, T2, T, &g, &t)], 1);
+    }
+    __syncthreads();
+    const int osl = tid / CH, och = tid % CH;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int r = osl; r < R; r += SNT / CH) {
+        const int n = cnt[r];
+        if (n > 0) {
+            const int64_t off_o = ((int64_t)bh * R + r) * D + och * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += (float)n * ma_load_f(op, off_o + e, op_dtype);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs.part[osl][och * 8 + e] = acc[e];
+    __syncthreads();
+    {
+        const int d = tid % D, q = tid / D;
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < CS::S / CS::QG; ++k) t += cs.part[q * (CS::S / CS::QG) + k][d];
+        cs.part2[q][d] = t;
+    }
+    __syncthreads();
+    if (tid < D) {
+        float t = 0.f;
+#pragma unroll
+        for (int q = 0; q < CS::QG; ++q) t += cs.part2[q][tid];
+        centre[(int64_t)bh * D + tid] = t / (float)R2;
+    }
 }
 
 }  // namespace
@@ -321,18 +599,28 @@ extern "C" int ma_value_centre(const void *op, int op_dtype, int B, int H, int G
         ma_set_error("ma_value_centre: bad arguments");
         return MA_EINVAL;
     }
+    if (((uintptr_t)op & 15) != 0) {
+        ma_set_error("ma_value_centre: op must be 16-byte aligned");
+        return MA_EINVAL;
+    }
+    if (G * T2 > MAX_R2 || G * T > MAX_R) {
+        ma_set_error("ma_value_centre: %d selection rows / %d rows per KV head exceed the built maximum %d / %d",
+                     G * T2, G * T, MAX_R2, MAX_R);
+        return MA_EUNSUPPORTED;
+    }
     if (D == 128)
-        hipLaunchKernelGGL(centre_kernel<128>, dim3(B * H), dim3(NT), 0, (hipStream_t)stream, op, op_dtype, G, T,
+        hipLaunchKernelGGL(centre_kernel<128>, dim3(B * H), dim3(SNT), 0, (hipStream_t)stream, op, op_dtype, G, T,
                            q_rows, T2, centre);
     else
-        hipLaunchKernelGGL(centre_kernel<64>, dim3(B * H), dim3(NT), 0, (hipStream_t)stream, op, op_dtype, G, T,
+        hipLaunchKernelGGL(centre_kernel<64>, dim3(B * H), dim3(SNT), 0, (hipStream_t)stream, op, op_dtype, G, T,
                            q_rows, T2, centre);
     return ma_check_launch("ma_value_centre");
 }
 
 extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
                                 const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
-                                int op_dtype, float scale, int value, int v_round_bf16, float *mass, float *score, void *stream) {
+                                int op_dtype, float scale, int value, int v_round_bf16, float *mass, float *score,
+                                void *stream) {
     const char *who = "ma_prefix_scores";
     int rc = ma_validate_prefix(p, D, who);
     if (rc) return rc;
@@ -346,18 +634,35 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
         ma_set_error("%s: query must be 16-byte aligned with aligned row strides", who);
         return MA_EINVAL;
     }
+    if (value && ((uintptr_t)op & 15)) {
+        ma_set_error("%s: the prefix output O_p must be 16-byte aligned", who);
+        return MA_EINVAL;
+    }
     const int G = Hq / H, R = G * T, R2 = G * T2;
     const int row_tiles = (R2 + 31) / 32;
-    if (row_tiles > 2 * MAX_WAVES) {
-        ma_set_error("%s: %d selection rows per KV head exceed the built maximum %d", who, R2, 64 * MAX_WAVES);
+    if (row_tiles > MAX_RT || R > MAX_R) {
+        ma_set_error("%s: %d selection rows / %d rows per KV head exceed the built maximum %d / %d", who, R2, R,
+                     MAX_R2, MAX_R);
         return MA_EUNSUPPORTED;
     }
     const int n = p->nq + p->nf;
     if (n == 0) return MA_OK;
-    const int rpw = (row_tiles + MAX_WAVES - 1) / MAX_WAVES;
+    // 16-bit parts are read with 32-byte vector loads: every token row must stay aligned
+    const bool dense_vec_ok = p->nf == 0 || (p->fdtype != MA_F32 && p->skf[2] % 16 == 0 && p->svf[2] % 16 == 0 &&
+                                             ((uintptr_t)p->kf & 15) == 0 && ((uintptr_t)p->vf & 15) == 0 &&
+                                             p->skf[0] % 16 == 0 && p->skf[1] % 16 == 0 && p->svf[0] % 16 == 0 &&
+                                             p->svf[1] % 16 == 0);
+    const int halves = row_tiles <= 8 ? 1 : 2;
     const int tiles = (n + TILE - 1) / TILE;
-    int per = (tiles * B * H + ma_num_cus() - 1) / ma_num_cus();
+    const bool packed = p->nq > 0;
+    // whole tiles of the source kind go to the pipelined workgroups, the rest (a tile
+    // straddling the packed / 16-bit boundary, 16-bit tail tiles, a partial last tile,
+    // f32 or unaligned 16-bit prefixes) to one tail workgroup each
+    int nfast = packed ? p->nq / TILE : n / TILE;
+    if (!dense_vec_ok) nfast = 0;
+    int per = nfast > 0 ? (nfast * B * H + ma_num_cus() - 1) / ma_num_cus() : 1;
     if (per < 1) per = 1;
+    const int fast_wgs = nfast > 0 ? (nfast + per - 1) / per : 0;
     ScoreArgs sa;
     sa.q = q;
     sa.pre = prefix_dev(p);
@@ -375,22 +680,29 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     sa.R = R;
     sa.R2 = R2;
     sa.row_tiles = row_tiles;
-    sa.tiles_per_wg = per;
     sa.value = value;
     sa.vround = v_round_bf16;
+    sa.nfast = nfast;
+    sa.per = per;
+    sa.fast_wgs = fast_wgs;
     sa.sl2 = scale * MA_LOG2E;
-    dim3 grid((tiles + per - 1) / per, B * H);
-    dim3 block(NT);
+    dim3 grid(fast_wgs + (tiles - nfast), B * H);
+    dim3 block(SNT);
     hipStream_t st = (hipStream_t)stream;
-    const bool packed = p->nq > 0;
-#define MA_SCORE(D_, R_, S_) hipLaunchKernelGGL((score_kernel<D_, R_, S_>), grid, block, 0, st, sa)
+#define MA_SCORE(D_, S_, H_) hipLaunchKernelGGL((score_kernel<D_, S_, H_>), grid, block, 0, st, sa)
+#define MA_SCORE_I(D_, S_)                        \
+    do {                                          \
+        if (halves == 1) MA_SCORE(D_, S_, 1);     \
+        else MA_SCORE(D_, S_, 2);                 \
+    } while (0)
     if (D == 128) {
-        if (rpw == 1) { if (packed) MA_SCORE(128, 1, SRC_PACKED); else MA_SCORE(128, 1, SRC_DENSE); }
-        else { if (packed) MA_SCORE(128, 2, SRC_PACKED); else MA_SCORE(128, 2, SRC_DENSE); }
+        if (packed) MA_SCORE_I(128, SRC_PACKED);
+        else MA_SCORE_I(128, SRC_DENSE);
     } else {
-        if (rpw == 1) { if (packed) MA_SCORE(64, 1, SRC_PACKED); else MA_SCORE(64, 1, SRC_DENSE); }
-        else { if (packed) MA_SCORE(64, 2, SRC_PACKED); else MA_SCORE(64, 2, SRC_DENSE); }
+        if (packed) MA_SCORE_I(64, SRC_PACKED);
+        else MA_SCORE_I(64, SRC_DENSE);
     }
+#undef MA_SCORE_I
 #undef MA_SCORE
     return ma_check_launch(who);
 }
