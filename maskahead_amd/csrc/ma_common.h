@@ -113,6 +113,52 @@ __device__ __forceinline__ float ma_sum_xor32(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ---- DPP lane moves (GFX9 encodings): a lane reads lane i+n (row_shl) / i-n (row_shr)
+// inside its 16-lane row, or lane 15 / 31 of the previous row (row_bcast); lanes whose
+// source is outside the row read 0.  They go through the VALU, not the LDS crossbar that
+// __shfl_* uses, so a wave scan costs a few cycles per step instead of an LDS round trip.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t ma_dpp(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xf, true);
+}
+enum { MA_DPP_SHL1 = 0x101, MA_DPP_SHL2 = 0x102, MA_DPP_SHL4 = 0x104, MA_DPP_SHL8 = 0x108,
+       MA_DPP_SHR1 = 0x111, MA_DPP_SHR2 = 0x112, MA_DPP_SHR4 = 0x114, MA_DPP_SHR8 = 0x118,
+       MA_DPP_BCAST15 = 0x142, MA_DPP_BCAST31 = 0x143 };
+
+// inclusive prefix sum over the 64 lanes of the wave (lane i gets lanes 0..i); u32 wraps
+__device__ __forceinline__ uint32_t ma_wave_prefix_u32(uint32_t x) {
+    x += ma_dpp<MA_DPP_SHR1>(x);
+    x += ma_dpp<MA_DPP_SHR2>(x);
+    x += ma_dpp<MA_DPP_SHR4>(x);
+    x += ma_dpp<MA_DPP_SHR8>(x);
+    x += ma_dpp<MA_DPP_BCAST15, 0xa>(x);   // rows 1, 3 += last lane of rows 0, 2
+    x += ma_dpp<MA_DPP_BCAST31, 0xc>(x);   // rows 2, 3 += lane 31
+    return x;
+}
+// the same value in every lane: sum / max over the wave (u32)
+__device__ __forceinline__ uint32_t ma_wave_sum_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)ma_wave_prefix_u32(x), 63);
+}
+__device__ __forceinline__ uint32_t ma_wave_max_u32(uint32_t x) {
+    x = max(x, ma_dpp<MA_DPP_SHR1>(x));
+    x = max(x, ma_dpp<MA_DPP_SHR2>(x));
+    x = max(x, ma_dpp<MA_DPP_SHR4>(x));
+    x = max(x, ma_dpp<MA_DPP_SHR8>(x));
+    x = max(x, ma_dpp<MA_DPP_BCAST15, 0xa>(x));
+    x = max(x, ma_dpp<MA_DPP_BCAST31, 0xc>(x));
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+// sum of lanes i .. i+N-1 into lane i, for lanes i that are multiples of N (N = 2, 4, 8,
+// 16; groups do not cross a 16-lane row); ((x0 + x1) + (x2 + x3)) + ... order
+template <int N>
+__device__ __forceinline__ float ma_group_sum_first(float x) {
+    if constexpr (N >= 2) x += __uint_as_float(ma_dpp<MA_DPP_SHL1>(__float_as_uint(x)));
+    if constexpr (N >= 4) x += __uint_as_float(ma_dpp<MA_DPP_SHL2>(__float_as_uint(x)));
+    if constexpr (N >= 8) x += __uint_as_float(ma_dpp<MA_DPP_SHL4>(__float_as_uint(x)));
+    if constexpr (N >= 16) x += __uint_as_float(ma_dpp<MA_DPP_SHL8>(__float_as_uint(x)));
+    return x;
+}
+
 __device__ __forceinline__ f32x16_t ma_mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }

@@ -249,13 +249,10 @@ __device__ __forceinline__ float vg_dist(const Lane &L, int u, int n0, int end, 
     return acc;
 }
 
-// sum over the D/16 adjacent lanes of a token (xor tree: every lane of the group ends
-// with the same value)
+// sum over the D/16 adjacent lanes of a token, into the token's first lane (DPP row moves)
 template <int D>
 __device__ __forceinline__ float token_sum(float v) {
-#pragma unroll
-    for (int o = 1; o < D / 16; o <<= 1) v += __shfl_xor(v, o);
-    return v;
+    return ma_group_sum_first<D / 16>(v);
 }
 
 constexpr int MAX_R = 1024;   // query rows of a KV head (G * T)

@@ -4,15 +4,19 @@
 //     top (C - W) of the score among the others where sinks and pinned positions rank
 //     +inf, returned in position order.
 //
-// One workgroup (1024 threads) per row.  Element j = e*NT + tid lives in thread tid, slot
-// e, as a monotone 32-bit key (larger float -> larger key, -0.0 == +0.0, NaN above +inf,
-// padding 0 below every real key).  The k-th largest key T is found exactly by an LDS
-// histogram radix select over three digits (11 + 11 + 10 bits): per digit one pass of LDS
-// atomics over the keys that match the digits found so far, then a block-wide suffix
-// scan of the bins.  An element is selected if key > T, or key == T and fewer than
-// k - count(key > T) equal keys precede it in index order.  A block-wide exclusive scan of
-// the selection flags in index order gives every selected element its output slot, so the
-// output is ascending by construction -- no sort.
+// One workgroup (1024 threads) per row.  Thread t owns VPT/4 runs of 4 consecutive
+// elements, run q covering j = 4*(q*NT + t) + c (so a wave's 16-byte loads are one
+// contiguous 1 KB), held as monotone 32-bit keys (larger float -> larger key,
+// -0.0 == +0.0, NaN above +inf, padding 0 below every real key).
+// The k-th largest key T is found exactly by an LDS-histogram radix select whose 11-bit
+// digits start at the highest bit that varies among the keys above -inf; after the first
+// digit the keys of the boundary bin are kept in an LDS candidate list (appended with
+// one atomic per wave).  An element is selected if key > T, or key == T and fewer than
+// k - count(key > T) equal keys precede it in index order.  The output slot of a selected
+// element is one block-wide exclusive scan of per-(thread, run) counts plus its rank
+// inside the run: the output is ascending by
+// construction -- no sort.  (Index order is run-major: run q of every thread, then run
+// q + 1; the scans carry one count per run.)
 #include "ma_common.h"
 
 namespace {
@@ -20,15 +24,12 @@ namespace {
 constexpr int NT = 1024;
 constexpr int NW = NT / 64;
 constexpr int NBINS = 2048;
+constexpr int NHC = 4;        // histogram copies (wave w counts into copy w % 4)
+constexpr uint32_t KEY_NEG_INF = 0x007fffffu;   // ma_order_key(-inf); padding keys are 0
+constexpr int CAND_MAX = 4096;   // keys of the boundary bin kept in LDS after the first digit
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-constexpr int NHC = 4;        // histogram copies (wave w counts into copy w % 4)
-constexpr uint32_t KEY_NEG_INF = 0x007fffffu;   // ma_order_key(-inf); padding keys are 0
-
-constexpr int CAND_MAX = 4096;   // keys of the boundary bin kept in LDS after the first digit
-
-template <int VPT>
 struct SelectSmem {
     uint32_t hist[NHC][NBINS];
     uint32_t cand[CAND_MAX];
@@ -36,37 +37,70 @@ struct SelectSmem {
     int wsum[NW];
     uint32_t kred[2][NW];
     int found_digit, found_gt, found_cnt;
-    int c_eq[VPT][NW], c_sel[VPT][NW];
-    int p_eq[VPT + 1], p_sel[VPT + 1];
     int flag;
+    int rsum[16][NW];
 };
 
 // Block-wide inclusive suffix sum of v over thread order (thread t gets sum over t' >= t).
-template <int VPT>
-__device__ __forceinline__ int block_suffix_incl(int v, SelectSmem<VPT> &S) {
+__device__ __forceinline__ int block_suffix_incl(int v, SelectSmem &S) {
     const int lane = lane_id(), wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_down(v, o);
-        if (lane + o < 64) v += y;
-    }
-    if (lane == 0) S.wsum[wave] = v;   // lane 0 holds the wave total
+    const uint32_t pre = ma_wave_prefix_u32((uint32_t)v);          // lanes 0..lane
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)pre, 63);
+    if (lane == 0) S.wsum[wave] = (int)tot;
     __syncthreads();
     int above = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) above += (w > wave) ? S.wsum[w] : 0;
-    return v + above;
+    __syncthreads();   // wsum is reused
+    return (int)(tot - pre) + v + above;
+}
+
+// Exclusive prefix of per-(run, thread) counts c[q] in index order (run-major, then
+// thread): all NR runs are scanned at once, two runs per 32-bit word (a run holds at most
+// 4 * NT = 4096 elements, so 16-bit halves never carry), one barrier pair.
+template <int NR>
+__device__ __forceinline__ void block_prefix_runs(int (&c)[NR], SelectSmem &S) {
+    constexpr int NP = (NR + 1) / 2;
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    uint32_t incl[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+        incl[q] = (uint32_t)c[2 * q] | (2 * q + 1 < NR ? (uint32_t)c[2 * q + 1] << 16 : 0u);
+#pragma unroll
+    for (int q = 0; q < NP; ++q) incl[q] = ma_wave_prefix_u32(incl[q]);
+    if (lane == 63) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q) S.rsum[q][wave] = (int)incl[q];
+    }
+    __syncthreads();
+    int base = 0;   // counts of all earlier runs
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        uint32_t before = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const uint32_t x = (uint32_t)S.rsum[q][w];
+            before += (w < wave) ? x : 0u;
+            tot += x;
+        }
+        const uint32_t ex = before + incl[q];   // inclusive, both halves
+        const int lo = (int)(ex & 0xffffu) - c[2 * q], tlo = (int)(tot & 0xffffu);
+        c[2 * q] = base + lo;
+        base += tlo;
+        if (2 * q + 1 < NR) {
+            const int hi = (int)(ex >> 16) - c[2 * q + 1], thi = (int)(tot >> 16);
+            c[2 * q + 1] = base + hi;
+            base += thi;
+        }
+    }
+    __syncthreads();   // rsum is reused
 }
 
 // The k-th largest of the block's keys (1 <= k <= number of keys).  Returns T and sets
-// need = k - count(key > T), the number of keys equal to T that are selected.
-// The digits adapt to the keys' range: above the highest bit in which the largest key and
-// the smallest key above -inf differ, all those keys agree, so the first 11-bit digit
-// starts there (scores that span a few binades then spread over many bins instead of
-// piling into a few, which would serialize the LDS atomics).  Keys at -inf or below only
-// matter when fewer than k keys are above -inf; then T is -inf.
+// need = k - count(key > T), the number of keys equal to T that are selected, and eq =
+// count(key == T) (-1 when T is -inf and eq was not counted).
 template <int VPT>
-__device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT> &S, int &need, int &eq) {
+__device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem &S, int &need, int &eq) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // range of the keys above -inf, and how many there are
     uint32_t kmax = 0u, kmin = 0xffffffffu;
@@ -76,13 +110,11 @@ __device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT>
         const bool hi = key[e] > KEY_NEG_INF;
         kmax = max(kmax, key[e]);
         kmin = hi ? min(kmin, key[e]) : kmin;
-        nhi += __popcll(__ballot(hi));
+        nhi += hi ? 1 : 0;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
-        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
-    }
+    kmax = ma_wave_max_u32(kmax);
+    kmin = ~ma_wave_max_u32(~kmin);
+    nhi = (int)ma_wave_sum_u32((uint32_t)nhi);
     if (lane == 0) {
         S.kred[0][wave] = kmax;
         S.kred[1][wave] = kmin;
@@ -114,12 +146,14 @@ __device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT>
     int kk = k;
     bool listed = false;      // after the first digit: the boundary bin's keys are in S.cand
     int ncand = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll 1
     while (hi >= 0) {
         const int w = hi + 1 < 11 ? hi + 1 : 11;
         const int shift = hi - w + 1;
         const int nb = 1 << w;
         for (int i = tid; i < NHC * NBINS; i += NT) (&S.hist[0][0])[i] = 0u;
+        if (tid == 0) S.ncand = 0;
         __syncthreads();
         uint32_t *hist = S.hist[wave % NHC];
         if (!listed) {
@@ -143,7 +177,7 @@ __device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT>
                 c1 += (int)S.hist[c][b0 + 1];
             }
         }
-        const int incl = block_suffix_incl<VPT>(c0 + c1, S);
+        const int incl = block_suffix_incl(c0 + c1, S);
         const int above = incl - c0 - c1;  // keys with a digit above both of my bins
         if (above < kk && above + c1 >= kk) {
             S.found_digit = b0 + 1;
@@ -154,7 +188,6 @@ __device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT>
             S.found_gt = above + c1;
             S.found_cnt = c0;
         }
-        if (tid == 0) S.ncand = 0;
         __syncthreads();
         const uint32_t d = (uint32_t)S.found_digit;
         const int bin_cnt = S.found_cnt;
@@ -163,10 +196,19 @@ __device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT>
         pmask |= (uint32_t)(nb - 1) << shift;
         hi = shift - 1;
         if (!listed && hi >= 0 && bin_cnt <= CAND_MAX) {
-            // keep the boundary bin's keys in LDS; later digits read only those
+            // keep the boundary bin's keys in LDS (one atomic per wave and slot); later
+            // digits read only those
 #pragma unroll
-            for (int e = 0; e < VPT; ++e)
-                if ((key[e] & pmask) == prefix) S.cand[atomicAdd(&S.ncand, 1)] = key[e];
+            for (int e = 0; e < VPT; ++e) {
+                const bool in = (key[e] & pmask) == prefix;
+                const uint64_t m = __ballot(in);
+                if (m) {
+                    int base = 0;
+                    if (lane == 0) base = atomicAdd(&S.ncand, __popcll(m));
+                    base = __builtin_amdgcn_readfirstlane(base);
+                    if (in) S.cand[base + __popcll(m & below)] = key[e];
+                }
+            }
             __syncthreads();
             ncand = S.ncand;
             listed = true;
@@ -178,131 +220,118 @@ __device__ uint32_t radix_kth(const uint32_t (&key)[VPT], int k, SelectSmem<VPT>
     return prefix;
 }
 
-// Output slots of the selected keys (bit e of selbits: slot e of this thread) in index
-// order: counts per (slot, wave), an exclusive scan over them, then each selected key's
-// output slot = keys selected before it.
+// Select key > T or (key == T and among the first `need` equal keys in index order), then
+// emit(key, j, slot) for every selected element (its key, index j) with its output slot
+// in index order.
 template <int VPT, class Emit>
-__device__ __forceinline__ void select_emit(uint64_t selbits, SelectSmem<VPT> &S, Emit emit) {
-    const int wave = threadIdx.x >> 6, lane = lane_id();
-    const uint64_t below = (1ull << lane) - 1ull;
+__device__ void select_emit(const uint32_t (&key)[VPT], uint32_t thr, int need, int eq, SelectSmem &S, Emit emit) {
+    constexpr int NR = VPT / 4;
+    const int tid = threadIdx.x;
+    uint64_t selbits = 0;
+    if (eq == need) {
+        // every key equal to T is selected: no tie ranking needed
 #pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const uint64_t bs = __ballot((selbits >> e) & 1);
-        if (lane == 0) S.c_sel[e][wave] = __popcll(bs);
-    }
-    __syncthreads();
-    if (wave == 0) {
-        int tot = 0;
-        if (lane < VPT) {
-            for (int w = 0; w < NW; ++w) {
-                const int c = S.c_sel[lane][w];
-                S.c_sel[lane][w] = tot;
-                tot += c;
+        for (int e = 0; e < VPT; ++e) selbits |= (uint64_t)(key[e] >= thr) << e;
+    } else {
+        int eb[NR];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+            eb[q] = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) eb[q] += key[4 * q + c] == thr ? 1 : 0;
+        }
+        block_prefix_runs<NR>(eb, S);   // equal keys before each run
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = 4 * q + c;
+                const bool is_eq = key[e] == thr;
+                const bool sl = key[e] > thr || (is_eq && eb[q] < need);
+                eb[q] += is_eq ? 1 : 0;
+                selbits |= (uint64_t)sl << e;
             }
         }
-        int incl = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
-        }
-        if (lane < VPT) S.p_sel[lane] = incl - tot;
     }
-    __syncthreads();
+    int slot[NR];
 #pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const bool sl = (selbits >> e) & 1;
-        const uint64_t bs = __ballot(sl);
-        if (sl) emit(e, S.p_sel[e] + S.c_sel[e][wave] + __popcll(bs & below));
+    for (int q = 0; q < NR; ++q) slot[q] = __popcll((selbits >> (4 * q)) & 15ull);
+    block_prefix_runs<NR>(slot, S);
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = 4 * q + c;
+            if ((selbits >> e) & 1) {
+                emit(key[e], 4 * (q * NT + tid) + c, slot[q]);
+                ++slot[q];
+            }
+        }
     }
 }
 
-// Select key > T or (key == T and among the first `need` equal keys in index order), and
-// give every selected element its rank in index order.  Writes slot (or -1) per slot e.
-template <int VPT, class Emit>
-__device__ void select_and_rank(const uint32_t (&key)[VPT], uint32_t thr, int need, int eq, SelectSmem<VPT> &S,
-                                Emit emit) {
-    const int wave = threadIdx.x >> 6, lane = lane_id();
-    const uint64_t below = (1ull << lane) - 1ull;
-    if (eq == need) {
-        // every key equal to T is selected: no tie ranking needed
-        uint64_t selbits = 0;
-#pragma unroll
-        for (int e = 0; e < VPT; ++e) selbits |= (uint64_t)(key[e] >= thr) << e;
-        select_emit<VPT>(selbits, S, emit);
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const uint64_t be = __ballot(key[e] == thr);
-        if (lane == 0) S.c_eq[e][wave] = __popcll(be);
-    }
-    __syncthreads();
-    // wave 0, lane e: slot e's equal counts -> exclusive prefix over waves (in place) and,
-    // by a wave scan, over slots
-    if (wave == 0) {
-        int tot = 0;
-        if (lane < VPT) {
-            for (int w = 0; w < NW; ++w) {
-                const int c = S.c_eq[lane][w];
-                S.c_eq[lane][w] = tot;
-                tot += c;
-            }
-        }
-        int incl = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
-        }
-        if (lane < VPT) S.p_eq[lane] = incl - tot;
-    }
-    __syncthreads();
-    // tie rank of each equal key in index order
-    uint64_t selbits = 0;
-#pragma unroll
-    for (int e = 0; e < VPT; ++e) {
-        const bool is_eq = key[e] == thr;
-        const int eb = S.p_eq[e] + S.c_eq[e][wave] + __popcll(__ballot(is_eq) & below);
-        const bool sl = key[e] > thr || (is_eq && eb < need);
-        selbits |= (uint64_t)sl << e;
-    }
-    select_emit<VPT>(selbits, S, emit);
+// float of a key (inverse of ma_order_key; -0.0 and NaN payloads come back canonical)
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
+
+// The VPT elements of this thread (runs of 4, run q at 4*(q*NT + t)) as floats: 16-byte
+// loads when the row is aligned, clamped scalar loads otherwise.
+template <int VPT>
+__device__ __forceinline__ void load_runs(float (&v)[VPT], const float *row, int n, bool vec) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < VPT / 4; ++q) {
+        const int j0 = 4 * (q * NT + tid);
+        if (vec && j0 + 4 <= n) {
+            const f32x4_t x = *(const f32x4_t *)(row + j0);
+            v[4 * q] = x[0];
+            v[4 * q + 1] = x[1];
+            v[4 * q + 2] = x[2];
+            v[4 * q + 3] = x[3];
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[4 * q + c] = row[min(j0 + c, n - 1)];
+        }
+    }
+}
+
+__device__ __forceinline__ int elem_index(int e) { return 4 * ((e >> 2) * NT + (int)threadIdx.x) + (e & 3); }
 
 // ---------------------------------------------------------------- read set
 template <int VPT>
 __global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t rank_stride, const uint8_t *mask,
                                                   int64_t mask_stride, int n, int k, int64_t *idx,
-                                                  int64_t idx_stride, float *values) {
-    __shared__ SelectSmem<VPT> S;
+                                                  int64_t idx_stride, float *values, int vec) {
+    __shared__ SelectSmem S;
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *rr = rank + (int64_t)row * rank_stride;
     const uint8_t *mr = mask ? mask + (int64_t)row * mask_stride : nullptr;
     uint32_t key[VPT];
-    // branchless loads from clamped indices, 16 slots at a time in flight
+    {
+        float v[VPT];
+        load_runs<VPT>(v, rr, n, vec != 0);
 #pragma unroll
-    for (int e0 = 0; e0 < VPT; e0 += 16) {
-        constexpr int CH = VPT < 16 ? VPT : 16;
-        float v[CH];
-        uint8_t mb[CH];
-#pragma unroll
-        for (int e = 0; e < CH; ++e) v[e] = rr[min((e0 + e) * NT + tid, n - 1)];
-#pragma unroll
-        for (int e = 0; e < CH; ++e) mb[e] = mr ? mr[min((e0 + e) * NT + tid, n - 1)] : (uint8_t)1;
-#pragma unroll
-        for (int e = 0; e < CH; ++e)
-            key[e0 + e] = (e0 + e) * NT + tid < n ? ma_order_key(mb[e] ? v[e] : -INFINITY) : 0u;
+        for (int e = 0; e < VPT; ++e) {
+            const int j = elem_index(e);
+            const bool live = !mr || mr[min(j, n - 1)] != 0;
+            key[e] = j < n ? ma_order_key(live ? v[e] : -INFINITY) : 0u;
+        }
     }
     int need, eq;
     const uint32_t thr = radix_kth<VPT>(key, k, S, need, eq);
     int64_t *out = idx + (int64_t)row * idx_stride;
     float *vout = values ? values + (int64_t)row * k : nullptr;
-    select_and_rank<VPT>(key, thr, need, eq, S, [&](int e, int slot) {
+    select_emit<VPT>(key, thr, need, eq, S, [&](uint32_t ke, int j, int slot) {
         if (slot < k) {
-            const int j = e * NT + tid;
             out[slot] = j;
-            if (vout) vout[slot] = (mr && !mr[j]) ? -INFINITY : rr[j];
+            if (vout) {
+                // the selected value from its key; a zero or NaN key re-reads the element
+                // so that -0.0 and NaN payloads come back as stored
+                float x = key_value(ke);
+                if (x == 0.f || x != x) x = (mr && !mr[j]) ? -INFINITY : rr[j];
+                vout[slot] = x;
+            }
         }
     });
 }
@@ -318,8 +347,8 @@ __global__ void __launch_bounds__(NT) keep_kernel(const PosT *pos, int64_t pos_s
                                                   int64_t score_stride, int n, int capacity, int window,
                                                   int64_t sink_tokens, const int64_t *pin_lo_rows, int64_t pin_lo,
                                                   int64_t pin_hi, int has_pin, int64_t *keep, int64_t keep_stride,
-                                                  int32_t *status) {
-    __shared__ SelectSmem<VPT> S;
+                                                  int32_t *status, int vec) {
+    __shared__ SelectSmem S;
     const int row = blockIdx.x, tid = threadIdx.x;
     const PosT *pr = pos + (int64_t)row * pos_stride;
     const float *sr = score + (int64_t)row * score_stride;
@@ -332,25 +361,32 @@ __global__ void __launch_bounds__(NT) keep_kernel(const PosT *pos, int64_t pos_s
     uint32_t key[VPT];
     bool bad = false;
 #pragma unroll
-    for (int e0 = 0; e0 < VPT; e0 += 8) {
-        constexpr int CH = VPT < 8 ? VPT : 8;
-        PosT p[CH], pn[CH];
-        float v[CH];
+    for (int q = 0; q < VPT / 4; ++q) {
+        // run q: elements j0 .. j0+3, and the element before it for the order check
+        const int j0 = 4 * (q * NT + tid);
+        float v[4];
+        if (vec && j0 + 4 <= n) {
+            const f32x4_t x = *(const f32x4_t *)(sr + j0);
+            v[0] = x[0];
+            v[1] = x[1];
+            v[2] = x[2];
+            v[3] = x[3];
+        } else {
 #pragma unroll
-        for (int e = 0; e < CH; ++e) {
-            const int jc = min((e0 + e) * NT + tid, n - 1);
-            p[e] = pr[jc];
-            pn[e] = pr[min(jc + 1, n - 1)];
-            v[e] = sr[jc];
+            for (int c = 0; c < 4; ++c) v[c] = sr[min(j0 + c, n - 1)];
         }
+        PosT p[5];
+        p[0] = pr[min(max(j0 - 1, 0), n - 1)];
 #pragma unroll
-        for (int e = 0; e < CH; ++e) {
-            const int j = (e0 + e) * NT + tid;
-            bad |= (j + 1 < n) && !(p[e] < pn[e]);
-            float x = v[e];
-            if ((int64_t)p[e] < sink_tokens) x = INFINITY;
-            if (has_pin && (int64_t)p[e] >= plo && (int64_t)p[e] < pin_hi) x = INFINITY;
-            key[e0 + e] = j < m ? ma_order_key(x) : 0u;
+        for (int c = 0; c < 4; ++c) p[c + 1] = pr[min(j0 + c, n - 1)];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int j = j0 + c;
+            bad |= (j > 0 && j < n) && !(p[c] < p[c + 1]);
+            float x = v[c];
+            if ((int64_t)p[c + 1] < sink_tokens) x = INFINITY;
+            if (has_pin && (int64_t)p[c + 1] >= plo && (int64_t)p[c + 1] < pin_hi) x = INFINITY;
+            key[4 * q + c] = j < m ? ma_order_key(x) : 0u;
         }
     }
     if (bad) S.flag = 1;   // benign race: every writer stores 1
@@ -360,8 +396,8 @@ __global__ void __launch_bounds__(NT) keep_kernel(const PosT *pos, int64_t pos_s
     if (rest > 0) {
         int need, eq;
         const uint32_t thr = radix_kth<VPT>(key, rest, S, need, eq);
-        select_and_rank<VPT>(key, thr, need, eq, S, [&](int e, int slot) {
-            if (slot < rest) out[slot] = e * NT + tid;
+        select_emit<VPT>(key, thr, need, eq, S, [&](uint32_t, int j, int slot) {
+            if (slot < rest) out[slot] = j;
         });
     }
     for (int i = tid; i < w; i += NT) out[rest + i] = m + i;
@@ -389,9 +425,10 @@ extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint
     if (rows == 0 || k == 0) return MA_OK;
     hipStream_t st = (hipStream_t)stream;
     const int vpt = vpt_for(n);
+    const int vec = ((uintptr_t)rank & 15) == 0 && rank_stride % 4 == 0;
 #define MA_TOPK(V)                                                                                                \
     hipLaunchKernelGGL(topk_kernel<V>, dim3(rows), dim3(NT), 0, st, rank, rank_stride, mask, mask_stride, n, k, idx, \
-                       idx_stride, values)
+                       idx_stride, values, vec)
     switch (vpt) {
         case 4: MA_TOPK(4); break;
         case 8: MA_TOPK(8); break;
@@ -419,16 +456,17 @@ extern "C" int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_strid
     if (rows == 0 || capacity == 0) return MA_OK;
     hipStream_t st = (hipStream_t)stream;
     const int vpt = vpt_for(n);
+    const int vec = ((uintptr_t)score & 15) == 0 && score_stride % 4 == 0;
 #define MA_KEEP(V)                                                                                                  \
     do {                                                                                                            \
         if (pos_is_i64)                                                                                             \
             hipLaunchKernelGGL((keep_kernel<V, int64_t>), dim3(rows), dim3(NT), 0, st, (const int64_t *)pos,         \
                                pos_stride, score, score_stride, n, capacity, window, sink_tokens, pin_lo_rows, pin_lo, \
-                               pin_hi, has_pin, keep, keep_stride, status);                                          \
+                               pin_hi, has_pin, keep, keep_stride, status, vec);                                     \
         else                                                                                                        \
             hipLaunchKernelGGL((keep_kernel<V, int32_t>), dim3(rows), dim3(NT), 0, st, (const int32_t *)pos,         \
                                pos_stride, score, score_stride, n, capacity, window, sink_tokens, pin_lo_rows, pin_lo, \
-                               pin_hi, has_pin, keep, keep_stride, status);                                          \
+                               pin_hi, has_pin, keep, keep_stride, status, vec);                                     \
     } while (0)
     switch (vpt) {
         case 4: MA_KEEP(4); break;
