@@ -131,10 +131,19 @@ int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix 
 /* a9. read-set top-k (session.py:1429-1438, reference.py:369-393): for each of `rows`
  * rows, the k largest of rank[row, 0..n) -- dead slots (mask 0) rank -inf, ties go to
  * the smaller index, -0.0 equals +0.0 and NaN ranks above +inf -- written as ascending
- * int64 indices to idx[row*idx_stride + i]; values (optional) gets rank at those indices.
- * rank row stride rank_stride, mask (optional) row stride mask_stride. */
+ * int64 indices to idx[row*idx_stride + i]; values (optional, [rows][k] contiguous) gets
+ * rank at those indices.  rank row stride rank_stride, mask (optional) row stride
+ * mask_stride.  Three launches over ceil(n / 1024) workgroups per row (n <= 4M).
+ * state: ma_topk_state_bytes(rows) bytes (one 32 KB histogram block per row), 256-byte
+ * aligned, zero-filled before its first use; every call leaves the
+ * blocks of its rows zero again, so one state buffer of R blocks serves any number of
+ * calls of up to R rows ordered on one stream (calls that overlap in time need their own).
+ * workspace: ma_topk_workspace_bytes(rows, n) bytes of scratch, 256-byte aligned. */
+int64_t ma_topk_state_bytes(int rows);
+int64_t ma_topk_workspace_bytes(int rows, int n);
 int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, int64_t mask_stride,
                    int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values,
+                   void *state, int64_t state_bytes, void *workspace, int64_t workspace_bytes,
                    void *stream);
 
 /* a10. keep set of an eviction step (EvictionState.survivors, eviction.py:325-409, for the

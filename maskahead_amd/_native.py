@@ -73,7 +73,9 @@ SIGNATURES = {
     "ma_compact_workspace_bytes": (_I64, [_I, _I, _P, _I]),
     "ma_compact_tokens": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _I64P, _I, _P, _I64, _P]),
     "ma_append_tokens": (_I, [_T4, _T4, _I, _I, _I, _I, _I, _P]),
-    "ma_topk_select": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P, _P]),
+    "ma_topk_state_bytes": (_I64, [_I]),
+    "ma_topk_workspace_bytes": (_I64, [_I, _I]),
+    "ma_topk_select": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P]),
     "ma_gather_kv": (_I, [_PREF, _I, _I, _I, _P, _I64P, _I, _T4, _T4, _P]),
     "ma_quantize_keys": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),
     "ma_quantize_values": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),

@@ -544,7 +544,6 @@ __global__ void __launch_bounds__(SNT) centre_kernel(const void *op, int op_dtyp
     using CS = CentreSmem<D>;
     constexpr int CH = D / 8;
     __shared__ CS cs;
-    __shared__ float cen[D];
     __shared__ int cnt[MAX_R];
     const int bh = blockIdx.x, tid = threadIdx.x;
     const int R = G * T, R2 = G * T2;

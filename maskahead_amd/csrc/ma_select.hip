@@ -1,8 +1,6 @@
-// Per-row selection kernels with index-ascending tie-break:
-//   * read set  (session.py:1429-1438): rank.masked_fill(dead, -inf).topk(k), indices sorted;
-//   * keep set  (eviction.py:355-409, score-ranked policies): the W newest entries, plus the
-//     top (C - W) of the score among the others where sinks and pinned positions rank
-//     +inf, returned in position order.
+// Keep-set selection with index-ascending tie-break (eviction.py:355-409, score-ranked
+// policies): the W newest entries, plus the top (C - W) of the score among the others
+// where sinks and pinned positions rank +inf, returned in position order.
 //
 // One workgroup (1024 threads) per row.  Thread t owns VPT/4 runs of 4 consecutive
 // elements, run q covering j = 4*(q*NT + t) + c (so a wave's 16-byte loads are one
@@ -298,44 +296,6 @@ __device__ __forceinline__ void load_runs(float (&v)[VPT], const float *row, int
 
 __device__ __forceinline__ int elem_index(int e) { return 4 * ((e >> 2) * NT + (int)threadIdx.x) + (e & 3); }
 
-// ---------------------------------------------------------------- read set
-template <int VPT>
-__global__ void __launch_bounds__(NT) topk_kernel(const float *rank, int64_t rank_stride, const uint8_t *mask,
-                                                  int64_t mask_stride, int n, int k, int64_t *idx,
-                                                  int64_t idx_stride, float *values, int vec) {
-    __shared__ SelectSmem S;
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float *rr = rank + (int64_t)row * rank_stride;
-    const uint8_t *mr = mask ? mask + (int64_t)row * mask_stride : nullptr;
-    uint32_t key[VPT];
-    {
-        float v[VPT];
-        load_runs<VPT>(v, rr, n, vec != 0);
-#pragma unroll
-        for (int e = 0; e < VPT; ++e) {
-            const int j = elem_index(e);
-            const bool live = !mr || mr[min(j, n - 1)] != 0;
-            key[e] = j < n ? ma_order_key(live ? v[e] : -INFINITY) : 0u;
-        }
-    }
-    int need, eq;
-    const uint32_t thr = radix_kth<VPT>(key, k, S, need, eq);
-    int64_t *out = idx + (int64_t)row * idx_stride;
-    float *vout = values ? values + (int64_t)row * k : nullptr;
-    select_emit<VPT>(key, thr, need, eq, S, [&](uint32_t ke, int j, int slot) {
-        if (slot < k) {
-            out[slot] = j;
-            if (vout) {
-                // the selected value from its key; a zero or NaN key re-reads the element
-                // so that -0.0 and NaN payloads come back as stored
-                float x = key_value(ke);
-                if (x == 0.f || x != x) x = (mr && !mr[j]) ? -INFINITY : rr[j];
-                vout[slot] = x;
-            }
-        }
-    });
-}
-
 // ---------------------------------------------------------------- keep set
 // Row = one (layer, batch, KV head) lane with n live entries whose positions increase
 // strictly along the live axis (the eviction state's invariant: survivors are stored in
@@ -414,34 +374,6 @@ int vpt_for(int n) {
 }
 
 }  // namespace
-
-extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, int64_t mask_stride,
-                              int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values, void *stream) {
-    if (!rank || !idx || rows < 0 || n < 0 || k < 0 || k > n || idx_stride < k || rank_stride < n ||
-        (mask && mask_stride < n)) {
-        ma_set_error("ma_topk_select: bad arguments (rows=%d n=%d k=%d)", rows, n, k);
-        return MA_EINVAL;
-    }
-    if (rows == 0 || k == 0) return MA_OK;
-    hipStream_t st = (hipStream_t)stream;
-    const int vpt = vpt_for(n);
-    const int vec = ((uintptr_t)rank & 15) == 0 && rank_stride % 4 == 0;
-#define MA_TOPK(V)                                                                                                \
-    hipLaunchKernelGGL(topk_kernel<V>, dim3(rows), dim3(NT), 0, st, rank, rank_stride, mask, mask_stride, n, k, idx, \
-                       idx_stride, values, vec)
-    switch (vpt) {
-        case 4: MA_TOPK(4); break;
-        case 8: MA_TOPK(8); break;
-        case 16: MA_TOPK(16); break;
-        case 32: MA_TOPK(32); break;
-        case 64: MA_TOPK(64); break;
-        default:
-            ma_set_error("ma_topk_select: n=%d exceeds the built maximum %d", n, 64 * NT);
-            return MA_EUNSUPPORTED;
-    }
-#undef MA_TOPK
-    return ma_check_launch("ma_topk_select");
-}
 
 extern "C" int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const float *score,
                               int64_t score_stride, int rows, int n, int capacity, int window, int64_t sink_tokens,

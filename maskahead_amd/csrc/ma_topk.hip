@@ -1,0 +1,542 @@
+// Read-set top-k over many workgroups per row (session.py:1429-1438,
+// reference.py:369-393): rank.masked_fill(dead, -inf).topk(k) with its indices sorted,
+// ties at the k-th value going to the smaller index.
+//
+// A row is cut into C chunks of CS = 256 * VPT elements; workgroup (c, row) owns chunk c
+// in all three kernels, so a chunk is re-read from the L2 of the XCD that read it first.
+// Elements are monotone 32-bit keys (larger float -> larger key, -0.0 == +0.0, NaN above
+// +inf, dead slots -inf); the k-th largest key T is found digit by digit, 13 + 11 + 8 bits:
+//   1. hist:     every chunk adds its 13-bit histogram into the row's global histogram.
+//   2. boundary: every workgroup reads the row's histogram and finds the bin d0 holding
+//                the k-th key and how many keys of that bin are still to take (krem);
+//                it counts its chunk's keys above bin d0 and writes the keys of bin d0
+//                (key, index) to the chunk's candidate slots.
+//   3. emit:     every workgroup reads the row's candidates (typically about 1% of the
+//                row) and finds the remaining 19 bits of T (two LDS histograms), the
+//                number `need` of keys equal to T that are selected (the first `need` in
+//                index order) and, from all chunks' counts, its own output base and how
+//                many of its T-equal keys it takes; then it writes its selected indices,
+//                ascending, to idx[base ..]: a block scan in index order, staged in LDS,
+//                then contiguous stores.  It also clears its share of the row's histogram.
+// Kernel boundaries are the only synchronisation: no workgroup waits for, or hands a
+// result to, another inside a kernel (on this chip a device-scope fence or a returning
+// atomic costs microseconds).  The small row-wide decisions (d0; T, need and the chunk
+// bases) are recomputed by every workgroup of the row from the same data.
+// Row r's histogram is block r of a state buffer that must be zero before its first use;
+// each call clears its rows' blocks again, so a state buffer of R blocks serves every
+// later call of up to R rows.  Chunk records and candidates go to a scratch workspace.
+#include "ma_common.h"
+
+namespace {
+
+constexpr int TB = 256;                 // threads per workgroup
+constexpr int TW = TB / 64;             // waves per workgroup
+constexpr int D0_BITS = 13, D1_BITS = 11, D2_BITS = 8;
+constexpr int S0 = 32 - D0_BITS;        // shift of the level-0 digit (19)
+constexpr int S1 = S0 - D1_BITS;        // shift of the level-1 digit (8)
+constexpr int H0 = 1 << D0_BITS;        // 8192 level-0 bins
+constexpr int H1 = 1 << D1_BITS;        // 2048 level-1 bins
+constexpr int H2 = 1 << D2_BITS;        // 256 level-2 bins
+constexpr int MAX_CHUNKS = 1024;        // per row (4 chunks per thread in the chunk scans)
+constexpr int NCR = 8;                  // candidates per thread kept in registers by the emit kernel
+static_assert(D0_BITS + D1_BITS + D2_BITS == 32, "digits cover the key");
+
+// one row's block of the state buffer
+struct alignas(256) RowState {
+    uint32_t hist[H0];   // zero between calls
+};
+struct ChunkInfo {
+    uint32_t gt;      // keys of the chunk above bin d0
+    uint32_t ncand;   // keys of the chunk in bin d0 (its candidates)
+    uint32_t d0;      // the row's boundary bin and
+    uint32_t krem;    // how many of its keys are selected
+};
+
+struct TopkArgs {
+    const float *rank;
+    int64_t rank_stride;
+    const uint8_t *mask;
+    int64_t mask_stride;
+    int n, k, C, vec;
+    int64_t *idx;
+    int64_t idx_stride;
+    float *values;
+    RowState *state;     // [rows]
+    ChunkInfo *chunk;    // [rows][C]
+    uint2 *cand;         // [rows][C][CS]: (key, index) per chunk
+};
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// Element e of this thread in chunk c: run q = e / 4 of 4 consecutive elements at
+// c*CS + 4*(q*TB + t), so a wave's 16-byte loads are contiguous.  Index order inside the
+// chunk is run-major.
+template <int VPT>
+__device__ __forceinline__ int chunk_index(int c, int e) {
+    return c * (TB * VPT) + 4 * ((e >> 2) * TB + (int)threadIdx.x) + (e & 3);
+}
+
+// keys of this thread's elements; 0 (below every real key) past the end of the row
+template <int VPT>
+__device__ __forceinline__ void chunk_keys(const TopkArgs &a, int row, int c, uint32_t (&key)[VPT]) {
+    const float *rr = a.rank + (int64_t)row * a.rank_stride;
+    const uint8_t *mr = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
+#pragma unroll
+    for (int q = 0; q < VPT / 4; ++q) {
+        const int j0 = chunk_index<VPT>(c, 4 * q);
+        float v[4];
+        if (a.vec && j0 + 4 <= a.n) {
+            const f32x4_t x = *(const f32x4_t *)(rr + j0);
+            v[0] = x[0];
+            v[1] = x[1];
+            v[2] = x[2];
+            v[3] = x[3];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = j0 + i < a.n ? rr[j0 + i] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = j0 + i;
+            const bool live = !mr || (j < a.n && mr[j] != 0);
+            key[4 * q + i] = j < a.n ? ma_order_key(live ? v[i] : -INFINITY) : 0u;
+        }
+    }
+}
+
+// float of a key (inverse of ma_order_key; -0.0 and NaN payloads come back canonical)
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
+// Exclusive prefix, in index order (run-major), of per-(run, thread) counts c[q]; returns
+// the block total.  wsum: LDS [NR * TW].
+template <int NR>
+__device__ __forceinline__ uint32_t block_prefix_runs(uint32_t (&c)[NR], uint32_t *wsum) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    uint32_t incl[NR];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) incl[q] = ma_wave_prefix_u32(c[q]);
+    if (lane == 63) {
+#pragma unroll
+        for (int q = 0; q < NR; ++q) wsum[q * TW + wave] = incl[q];
+    }
+    __syncthreads();
+    uint32_t base = 0;
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+        uint32_t before = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < TW; ++w) {
+            const uint32_t x = wsum[q * TW + w];
+            before += w < wave ? x : 0u;
+            tot += x;
+        }
+        c[q] = base + before + incl[q] - c[q];
+        base += tot;
+    }
+    __syncthreads();   // wsum is reused
+    return base;
+}
+
+// Thread t holds the counts of bins [t*PB, (t+1)*PB).  Finds the bin d with
+// count(bins above d) < kk <= count(bins >= d) and stores d and count(bins above d) in
+// found[0], found[1] (LDS), visible to the whole block on return.  Requires
+// 1 <= kk <= total.
+template <int PB>
+__device__ __forceinline__ void find_digit(const uint32_t (&h)[PB], uint32_t kk, uint32_t *wsum, uint32_t *found) {
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    uint32_t s = 0;
+#pragma unroll
+    for (int b = 0; b < PB; ++b) s += h[b];
+    const uint32_t incl = ma_wave_prefix_u32(s);
+    if (lane == 63) wsum[wave] = incl;
+    if (tid == 0) {   // defined result should kk exceed the total
+        found[0] = 0u;
+        found[1] = 0u;
+    }
+    __syncthreads();
+    uint32_t before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < TW; ++w) {
+        const uint32_t x = wsum[w];
+        before += w < wave ? x : 0u;
+        tot += x;
+    }
+    uint32_t above = tot - (before + incl);   // keys in the bins of threads > t
+#pragma unroll
+    for (int b = PB - 1; b >= 0; --b) {
+        if (above < kk && above + h[b] >= kk) {
+            found[0] = (uint32_t)(tid * PB + b);
+            found[1] = above;
+        }
+        above += h[b];
+    }
+    __syncthreads();
+}
+
+// Level-0 histogram of the chunk added into the row's histogram.
+template <int VPT>
+__global__ void __launch_bounds__(TB) topk_hist_kernel(TopkArgs a) {
+    __shared__ uint32_t h[H0];
+    const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    for (int i = tid; i < H0 / 4; i += TB) ((uint4 *)h)[i] = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t key[VPT];
+    chunk_keys<VPT>(a, row, c, key);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < VPT; ++e)
+        if (key[e]) atomicAdd(&h[key[e] >> S0], 1u);
+    __syncthreads();
+    uint32_t *gh = a.state[row].hist;
+    for (int i = tid; i < H0; i += TB) {
+        const uint32_t x = h[i];
+        if (x) atomicAdd(&gh[i], x);
+    }
+}
+
+// d0 / krem from the row's histogram; the chunk's count above bin d0 and its candidates.
+template <int VPT>
+__global__ void __launch_bounds__(TB) topk_boundary_kernel(TopkArgs a) {
+    constexpr int CS = TB * VPT, PB = H0 / TB;
+    __shared__ uint32_t wsum[TW], found[2];
+    const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    // thread t: bins [32t, 32t + 32), loaded together with the chunk's keys
+    uint32_t cnt[PB];
+    const uint4 *g4 = (const uint4 *)(a.state[row].hist + tid * PB);
+#pragma unroll
+    for (int i = 0; i < PB / 4; ++i) {
+        const uint4 x = g4[i];
+        cnt[4 * i] = x.x;
+        cnt[4 * i + 1] = x.y;
+        cnt[4 * i + 2] = x.z;
+        cnt[4 * i + 3] = x.w;
+    }
+    uint32_t key[VPT];
+    chunk_keys<VPT>(a, row, c, key);
+    find_digit<PB>(cnt, (uint32_t)a.k, wsum, found);
+    const uint32_t d0 = found[0], krem = (uint32_t)a.k - found[1];
+    uint32_t packed[1] = {0u};   // low 16 bits: keys above bin d0; high: keys in bin d0
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+        const uint32_t d = key[e] >> S0;
+        packed[0] += key[e] && d > d0 ? 1u : 0u;
+        packed[0] += key[e] && d == d0 ? 0x10000u : 0u;
+    }
+    const uint32_t total = block_prefix_runs<1>(packed, wsum);
+    uint2 *L = a.cand + ((int64_t)row * a.C + c) * CS;
+    uint32_t pos = packed[0] >> 16;
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+        if (key[e] && (key[e] >> S0) == d0) {
+            L[pos] = make_uint2(key[e], (uint32_t)chunk_index<VPT>(c, e));
+            ++pos;
+        }
+    }
+    if (tid == 0) {
+        ChunkInfo ci;
+        ci.gt = total & 0xffffu;
+        ci.ncand = total >> 16;
+        ci.d0 = d0;
+        ci.krem = krem;
+        a.chunk[(int64_t)row * a.C + c] = ci;
+    }
+}
+
+struct EmitSmem {
+    uint32_t hist[H1];
+    uint32_t pre[MAX_CHUNKS + 1];   // candidates of the chunks before chunk c
+    uint32_t acnt[MAX_CHUNKS];      // per chunk: candidates above T
+    uint32_t ecnt[MAX_CHUNKS];      // per chunk: candidates equal to T
+    uint32_t wsum[4 * TW], found[2];   // (block_prefix_runs<NR> uses NR * TW)
+    uint32_t base, take, eq;        // this workgroup's chunk
+};
+
+// T, need and the chunk's base from the row's candidates; the chunk's selected indices,
+// ascending, to idx[base ..]; values optional.
+template <int VPT>
+__global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
+    constexpr int NR = VPT / 4, CS = TB * VPT;
+    __shared__ EmitSmem S;
+    __shared__ uint32_t sj[CS], sk[CS];
+    const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, C = a.C;
+    const ChunkInfo *info = a.chunk + (int64_t)row * C;
+    // chunk records of chunks [4t, 4t + 4) and the chunk's keys, loads in flight together
+    uint32_t gt[4], nc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ch = 4 * tid + i;
+        gt[i] = 0u;
+        nc[i] = 0u;
+        if (ch < C) {
+            const ChunkInfo x = info[ch];
+            gt[i] = x.gt;
+            nc[i] = x.ncand;
+        }
+    }
+    const uint32_t d0 = info[0].d0, krem = info[0].krem;
+    uint32_t key[VPT];
+    chunk_keys<VPT>(a, row, c, key);
+    uint32_t run[1] = {nc[0] + nc[1] + nc[2] + nc[3]};
+    const uint32_t NC = block_prefix_runs<1>(run, S.wsum);
+    {
+        uint32_t p = run[0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ch = 4 * tid + i;
+            if (ch < C) S.pre[ch] = p;
+            p += nc[i];
+        }
+    }
+    if (tid == 0) S.pre[C] = NC;
+    for (int i = tid; i < H1; i += TB) S.hist[i] = 0u;
+    for (int i = tid; i < C; i += TB) {
+        S.acnt[i] = 0u;
+        S.ecnt[i] = 0u;
+    }
+    __syncthreads();
+    // candidate g of the row: chunk ch with pre[ch] <= g < pre[ch + 1], slot g - pre[ch]
+    const uint2 *L = a.cand + (int64_t)row * C * CS;
+    auto locate = [&](uint32_t g) {
+        int lo = 0, hi = C - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (S.pre[mid] <= g) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    const bool inreg = NC <= (uint32_t)(NCR * TB);
+    uint32_t ck[NCR], cc[NCR];
+    if (inreg) {
+#pragma unroll
+        for (int i = 0; i < NCR; ++i) {
+            const uint32_t g = tid + i * TB;
+            ck[i] = 0u;   // no candidate (candidate keys are real keys, never 0)
+            cc[i] = 0u;
+            if (g < NC) {
+                const int ch = locate(g);
+                ck[i] = L[(int64_t)ch * CS + (g - S.pre[ch])].x;
+                cc[i] = (uint32_t)ch;
+            }
+        }
+    }
+    auto each = [&](auto f) {
+        if (inreg) {
+#pragma unroll
+            for (int i = 0; i < NCR; ++i)
+                if (ck[i]) f(ck[i], cc[i]);
+        } else {
+            for (uint32_t g = tid; g < NC; g += TB) {
+                const int ch = locate(g);
+                f(L[(int64_t)ch * CS + (g - S.pre[ch])].x, (uint32_t)ch);
+            }
+        }
+    };
+    // level 1: bits [S1, S0) of the candidates
+    each([&](uint32_t x, uint32_t) { atomicAdd(&S.hist[(x >> S1) & (H1 - 1)], 1u); });
+    __syncthreads();
+    uint32_t d1, kr = krem;
+    {
+        constexpr int PB = H1 / TB;
+        uint32_t cnt[PB];
+#pragma unroll
+        for (int b = 0; b < PB; ++b) cnt[b] = S.hist[tid * PB + b];
+        find_digit<PB>(cnt, kr, S.wsum, S.found);
+        d1 = S.found[0];
+        kr -= S.found[1];
+    }
+    // level 2: the low bits of the candidates whose level-1 digit is d1
+    for (int i = tid; i < H2; i += TB) S.hist[i] = 0u;
+    __syncthreads();
+    each([&](uint32_t x, uint32_t) {
+        if (((x >> S1) & (H1 - 1)) == d1) atomicAdd(&S.hist[x & (H2 - 1)], 1u);
+    });
+    __syncthreads();
+    uint32_t thr, need;
+    {
+        uint32_t cnt[1] = {S.hist[tid]};
+        find_digit<1>(cnt, kr, S.wsum, S.found);
+        thr = (d0 << S0) | (d1 << S1) | S.found[0];
+        need = kr - S.found[1];
+    }
+    // per chunk: candidates above / equal to T
+    each([&](uint32_t x, uint32_t ch) {
+        if (x > thr) atomicAdd(&S.acnt[ch], 1u);
+        else if (x == thr) atomicAdd(&S.ecnt[ch], 1u);
+    });
+    __syncthreads();
+    // chunks [4t, 4t + 4): keys equal to T are taken in chunk order
+    {
+        uint32_t e[4], sel[4], ex[1] = {0u}, sx[1] = {0u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ch = 4 * tid + i;
+            e[i] = ch < C ? S.ecnt[ch] : 0u;
+            ex[0] += e[i];
+        }
+        block_prefix_runs<1>(ex, S.wsum);
+        uint32_t ebefore = ex[0];
+        uint32_t take[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ch = 4 * tid + i;
+            take[i] = need > ebefore ? min(need - ebefore, e[i]) : 0u;
+            ebefore += e[i];
+            sel[i] = ch < C ? gt[i] + S.acnt[ch] + take[i] : 0u;
+            sx[0] += sel[i];
+        }
+        block_prefix_runs<1>(sx, S.wsum);
+        uint32_t base = sx[0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * tid + i == c) {
+                S.base = base;
+                S.take = take[i];
+                S.eq = e[i];
+            }
+            base += sel[i];
+        }
+    }
+    // this workgroup's share of the row's histogram, cleared for the next call (the
+    // boundary kernel, its only reader, has finished)
+    for (int b = c * TB + tid; b < H0; b += C * TB) a.state[row].hist[b] = 0u;
+    __syncthreads();
+    const uint32_t cbase = S.base, ctake = S.take, ceq = S.eq;
+    uint32_t selbits = 0;
+    if (ctake == 0u || ctake >= ceq) {
+        // none or all of the chunk's keys equal to T (padding keys 0 lie below any T)
+        const bool all_eq = ctake != 0u;
+#pragma unroll
+        for (int e = 0; e < VPT; ++e) selbits |= (uint32_t)(key[e] > thr || (all_eq && key[e] == thr)) << e;
+    } else {
+        // the first `take` keys equal to T in index order
+        uint32_t eb[NR];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+            eb[q] = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) eb[q] += key[4 * q + i] == thr ? 1u : 0u;
+        }
+        block_prefix_runs<NR>(eb, S.wsum);
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 4 * q + i;
+                const bool is_eq = key[e] == thr;
+                selbits |= (uint32_t)(key[e] > thr || (is_eq && eb[q] < ctake)) << e;
+                eb[q] += is_eq ? 1u : 0u;
+            }
+        }
+    }
+    uint32_t slot[NR];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) slot[q] = __popc((selbits >> (4 * q)) & 15u);
+    const uint32_t nsel = block_prefix_runs<NR>(slot, S.wsum);
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * q + i;
+            if ((selbits >> e) & 1u) {
+                sj[slot[q]] = (uint32_t)chunk_index<VPT>(c, e);
+                sk[slot[q]] = key[e];
+                ++slot[q];
+            }
+        }
+    }
+    __syncthreads();
+    int64_t *out = a.idx + (int64_t)row * a.idx_stride + cbase;
+    float *vout = a.values ? a.values + (int64_t)row * a.k + cbase : nullptr;
+    const float *rr = a.rank + (int64_t)row * a.rank_stride;
+    const uint8_t *mr = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
+    // (cbase + nsel <= k by construction; the bound keeps inconsistent inputs from
+    // writing past the row)
+    const uint32_t nout = cbase < (uint32_t)a.k ? min(nsel, (uint32_t)a.k - cbase) : 0u;
+    for (uint32_t i = tid; i < nout; i += TB) {
+        const uint32_t j = sj[i];
+        out[i] = (int64_t)j;
+        if (vout) {
+            // the selected value from its key; a zero or NaN key re-reads the element so
+            // that -0.0 and NaN payloads come back as stored
+            float x = key_value(sk[i]);
+            if (x == 0.f || x != x) x = (mr && !mr[j]) ? -INFINITY : rr[j];
+            vout[i] = x;
+        }
+    }
+}
+
+int topk_vpt(int n) { return n <= TB * 4 * MAX_CHUNKS ? 4 : (n <= TB * 16 * MAX_CHUNKS ? 16 : 0); }
+
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+int64_t chunk_bytes(int rows, int n) {
+    const int vpt = topk_vpt(n);
+    return align256((int64_t)rows * ((n + TB * vpt - 1) / (TB * vpt)) * (int64_t)sizeof(ChunkInfo));
+}
+
+}  // namespace
+
+extern "C" int64_t ma_topk_state_bytes(int rows) {
+    return rows > 0 ? (int64_t)rows * (int64_t)sizeof(RowState) : 0;
+}
+
+extern "C" int64_t ma_topk_workspace_bytes(int rows, int n) {
+    if (rows <= 0 || n <= 0 || !topk_vpt(n)) return 0;
+    const int vpt = topk_vpt(n);
+    const int64_t C = (n + TB * vpt - 1) / (TB * vpt);
+    return chunk_bytes(rows, n) + align256((int64_t)rows * C * TB * vpt * (int64_t)sizeof(uint2));
+}
+
+extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, int64_t mask_stride,
+                              int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values,
+                              void *state, int64_t state_bytes, void *workspace, int64_t workspace_bytes,
+                              void *stream) {
+    if (!rank || !idx || rows < 0 || n < 0 || k < 0 || k > n || idx_stride < k || rank_stride < n ||
+        (mask && mask_stride < n) || rows > 65535) {
+        ma_set_error("ma_topk_select: bad arguments (rows=%d n=%d k=%d)", rows, n, k);
+        return MA_EINVAL;
+    }
+    if (rows == 0 || k == 0) return MA_OK;
+    const int vpt = topk_vpt(n);
+    if (!vpt) {
+        ma_set_error("ma_topk_select: n=%d exceeds the built maximum %d", n, TB * 16 * MAX_CHUNKS);
+        return MA_EUNSUPPORTED;
+    }
+    const int64_t need_state = ma_topk_state_bytes(rows), need_ws = ma_topk_workspace_bytes(rows, n);
+    if (!state || state_bytes < need_state || ((uintptr_t)state & 255) || !workspace ||
+        workspace_bytes < need_ws || ((uintptr_t)workspace & 255)) {
+        ma_set_error("ma_topk_select: state of %lld and workspace of %lld bytes (256-byte aligned) needed, "
+                     "got %lld and %lld", (long long)need_state, (long long)need_ws, (long long)state_bytes,
+                     (long long)workspace_bytes);
+        return MA_EINVAL;
+    }
+    TopkArgs a;
+    a.rank = rank;
+    a.rank_stride = rank_stride;
+    a.mask = mask;
+    a.mask_stride = mask_stride;
+    a.n = n;
+    a.k = k;
+    a.C = (n + TB * vpt - 1) / (TB * vpt);
+    a.vec = ((uintptr_t)rank & 15) == 0 && rank_stride % 4 == 0;
+    a.idx = idx;
+    a.idx_stride = idx_stride;
+    a.values = values;
+    a.state = (RowState *)state;
+    a.chunk = (ChunkInfo *)workspace;
+    a.cand = (uint2 *)((char *)workspace + chunk_bytes(rows, n));
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid(a.C, rows);
+    if (vpt == 4) {
+        hipLaunchKernelGGL(topk_hist_kernel<4>, grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL(topk_boundary_kernel<4>, grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL(topk_emit_kernel<4>, grid, dim3(TB), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(topk_hist_kernel<16>, grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL(topk_boundary_kernel<16>, grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL(topk_emit_kernel<16>, grid, dim3(TB), 0, st, a);
+    }
+    return ma_check_launch("ma_topk_select");
+}

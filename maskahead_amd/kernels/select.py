@@ -1,8 +1,14 @@
 """Per-row selection kernels: the read-set top-k (session.py:1429-1438).
 
 ``topk_ascending`` replaces ``rank.masked_fill(dead, -inf).topk(k).indices.sort()``
-with one kernel launch per call; ties at the k-th value go to the smaller index, so the
-result is deterministic (torch.topk leaves that order unspecified).
+with three kernel launches per call; ties at the k-th value go to the smaller index, so
+the result is deterministic (torch.topk leaves that order unspecified).
+
+The kernels keep each row's histogram in a state block that must be zero before its
+first use and that every call leaves zero again.  One state buffer per device is kept here
+and grown (zero-filled) when a call has more rows.  Calls share it, so calls that overlap
+in time (on two streams at once) must pass their own ``state``.  The scratch workspace is
+per call.
 """
 
 from __future__ import annotations
@@ -11,12 +17,27 @@ import torch
 
 from .. import _native as N
 
+_STATES: dict = {}
+
+
+def _state(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The zero-initialised select state of `device`, at least nbytes."""
+    st = _STATES.get(device.index)
+    if st is None or st.numel() < nbytes:
+        # the old one goes back to the caching allocator, which reuses it in stream order
+        st = torch.zeros((nbytes,), device=device, dtype=torch.uint8)
+        _STATES[device.index] = st
+    return st
+
 
 def topk_ascending(rank: torch.Tensor, k: int, mask: torch.Tensor | None = None, *,
-                   out: torch.Tensor | None = None, values: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None, values: torch.Tensor | None = None,
+                   state: torch.Tensor | None = None) -> torch.Tensor:
     """rank [..., n] f32 on the GPU -> int64 [..., k] ascending indices of the k
     largest entries per row; mask (uint8/bool [..., n], 0 = dead) ranks an entry -inf.
-    ``values`` (optional, f32 [..., k] contiguous) receives rank at those indices."""
+    ``values`` (optional, f32 [..., k] contiguous) receives rank at those indices.
+    ``state`` (optional, uint8, zero-filled before its first use, 256-byte aligned) replaces
+    the device's shared select state."""
     N.require_gpu(rank, "rank")
     if rank.dtype != torch.float32:
         raise ValueError("rank must be float32")
@@ -45,8 +66,15 @@ def topk_ascending(rank: torch.Tensor, k: int, mask: torch.Tensor | None = None,
     if values is not None and (not values.is_contiguous() or values.numel() != rows * k):
         raise ValueError("values must be a contiguous f32 [..., k] tensor")
     lib = N.load()
+    ws_bytes = int(lib.ma_topk_workspace_bytes(rows, n))
+    if ws_bytes <= 0:
+        raise N.KernelUnavailableError(f"ma_topk_select: n={n} exceeds the built maximum")
+    stream = N.stream_of(rank)
+    st = state if state is not None else _state(rank.device, int(lib.ma_topk_state_bytes(rows)))
+    ws = torch.empty((ws_bytes,), device=rank.device, dtype=torch.uint8)
     rc = lib.ma_topk_select(r2.data_ptr(), r2.stride(0) if rows > 1 else n, N.ptr(m2),
                             (m2.stride(0) if rows > 1 else n) if m2 is not None else 0, rows, n, k,
-                            o2.data_ptr(), o2.stride(0) if rows > 1 else k, N.ptr(values), N.stream_of(rank))
+                            o2.data_ptr(), o2.stride(0) if rows > 1 else k, N.ptr(values), st.data_ptr(),
+                            st.numel(), ws.data_ptr(), ws.numel(), stream)
     N.check(rc, "ma_topk_select")
     return out

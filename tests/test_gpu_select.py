@@ -39,3 +39,48 @@ def test_topk_batched_shape(gpu):
     assert got.shape == (2, 3, 100)
     want = x.topk(100, dim=-1).indices.sort(dim=-1).values
     assert torch.equal(got.cpu(), want)
+
+
+@pytest.mark.parametrize("n,k,rows", [(131072, 2048, 4), (1_100_003, 70001, 2)])
+def test_topk_large_rows(gpu, n, k, rows):
+    """Rows past one workgroup's reach: 128 chunks of 1024 (config 4's longest prefix), and
+    the 4096-element chunks used above 1M entries."""
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn((rows, n), generator=g).exp()
+    x[:, ::5] = (x[:, ::5] * 4).round() / 4           # ties across chunks
+    mask = (torch.rand((rows, n), generator=g) > 0.05).to(torch.uint8)
+    got = topk_ascending(x.to(gpu), k, mask.to(gpu))
+    assert torch.equal(got.cpu(), OS.topk_ascending(x, k, mask))
+
+
+def test_topk_all_equal_and_special_values(gpu):
+    """Every key in the boundary bin (the whole row equal), ties taken across many
+    chunks in index order; NaN above +inf; -inf rows; -0.0 == +0.0."""
+    n = 20000
+    rows = torch.zeros((6, n))
+    rows[1] = 1.5                                      # all equal: candidates = the row
+    rows[2] = float("-inf")                            # all dead-equivalent
+    rows[3, ::3] = float("nan")
+    rows[3, 1::3] = float("inf")
+    rows[4, ::2] = -0.0                                # +0.0 / -0.0 mix
+    rows[5] = torch.arange(n, dtype=torch.float32) % 7
+    for k in (1, 999, 12345, n):
+        got = topk_ascending(rows.to(gpu), k)
+        assert torch.equal(got.cpu(), OS.topk_ascending(rows, k)), k
+
+
+def test_topk_workspace_reuse_and_unaligned(gpu):
+    """Consecutive calls of different row counts and sizes share one state buffer (each
+    call leaves its rows' blocks zero); an unaligned, strided row view takes the scalar
+    load path."""
+    g = torch.Generator().manual_seed(5)
+    base = torch.rand((7, 40001), generator=g)
+    for rows, n, k in ((3, 40000, 3000), (7, 777, 50), (1, 40000, 1), (5, 5000, 5000), (7, 40000, 39999),
+                       (2, 12345, 600)):
+        x = base[:rows, 1:n + 1]
+        want = OS.topk_ascending(x.contiguous(), k)
+        got = topk_ascending(x.to(gpu), k)                    # contiguous copy, 16-byte loads
+        assert torch.equal(got.cpu(), want), (rows, n, k)
+        xg = base.to(gpu)[:rows, 1:n + 1]                     # 4-byte offset, row stride 40001
+        got = topk_ascending(xg, k)
+        assert torch.equal(got.cpu(), want), (rows, n, k, "view")

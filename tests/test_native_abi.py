@@ -46,7 +46,7 @@ def test_ctypes_table_matches_header():
 def test_version_and_error_mapping(lib):
     assert lib.ma_version() >= 1
     # k > n: rejected on the host before any launch
-    rc = lib.ma_topk_select(1, 8, None, 0, 1, 8, 9, 1, 9, None, None)
+    rc = lib.ma_topk_select(1, 8, None, 0, 1, 8, 9, 1, 9, None, None, 0, None, 0, None)
     assert rc == N.MA_EINVAL
     assert b"bad arguments" in lib.ma_last_error()
     with pytest.raises(ValueError):
