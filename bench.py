@@ -1,17 +1,21 @@
-"""Benchmark of the MI355X read path: step 0 of one sparse layer at the headline shape.
+"""Benchmark of the MI355X read path: step 0 of a sparse layer at the headline shape.
 
 Workload: packed int4 k4v4 cache, prefix 32768 tokens, batch
 1, 28 query / 4 KV heads, head_dim 128, mask block of 32 queries (all 32 are selection
-rows), read budget 2048 per KV head.  One step = split-K attention over [prefix | block]
-with prefix statistics, the value-aware score pass, the read-set top-k and the gather of
-the selected K/V into the compact bf16 buffer -- everything step 0 of the reference's
-fast path does for a sparse layer (session.py:1403-1454).  Inputs are synthetic (seeded
-N(0,1), LogNormal key channels, 4 sink keys x8) and resident in HBM before timing.
+rows), read budget 2048 per KV head.  One layer step = split-K attention over
+[prefix | block] with prefix statistics, the value-aware score pass, the read-set top-k
+and the gather of the selected K/V into the layer's compact bf16 buffer -- everything
+step 0 of the reference's fast path does for a sparse layer (session.py:1403-1454).
 
-The step is captured once in a HIP graph and replayed; the dominant kernel (split-K
-pass 1) is also timed alone from its own graph.  Prints ONE JSON line.
+One timed step is that layer step for each of --layers layers (28: the layer count of the
+7B-class model of configs 1 and 4), each layer with its own packed cache (the tokens of
+one seeded cache rolled by a per-layer offset), so no layer reads K/V left warm by the
+previous one; the reported per-layer time is the step time / layers.  Inputs are
+synthetic (seeded N(0,1), LogNormal key channels, 4 sink keys x8) and resident in HBM
+before timing.  The step is captured once in a HIP graph and replayed; the dominant
+kernel (split-K pass 1) is also timed alone from its own graph.  Prints ONE JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--split-tokens S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--layers L] [--split-tokens S] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -42,6 +46,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--layers", type=int, default=28, help="layers per timed step, each with its own cache")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall-clock budget of the CPU baseline sample (repeated whole steps)")
@@ -162,38 +167,53 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     q, k, v, kc, vc = layer_inputs(sh, dtype=torch.bfloat16)
-    lay = packed_layout(sh.b, sh.hkv, sh.n, sh.d, device=dev)
-    quantize_key_groups_into(k.to(dev), lay["kq"], lay["ks"], lay["kz"], bits=4, token_group=32)
-    quantize_values_into(v.to(dev), lay["vq"], lay["vs"], lay["vz"], bits=4, channel_group=32)
-    prefix = Prefix(kq=lay["kq"], ks=lay["ks"], kz=lay["kz"], vq=lay["vq"], vs=lay["vs"], vz=lay["vz"],
-                    nq=sh.n, kb=4, vb=4)
     qg, kcg, vcg = q.to(dev), kc.to(dev), vc.to(dev)
+    kdev, vdev = k.to(dev), v.to(dev)
     rows = torch.arange(sh.t, dtype=torch.int32, device=dev)
-    compact_k = torch.empty((sh.b, sh.hkv, sh.read_k + sh.t, sh.d), dtype=torch.bfloat16, device=dev)
-    compact_v = torch.empty_like(compact_k)
 
     class View:
+        """the packed cache of one layer, as the gather reads it (cache.py:LayerView)"""
         k_bits = v_bits = 4
         length = quantized_length = sh.n
         residual_length = 0
         key_token_group = value_channel_group = 32
-        k_q, k_scale, k_zero = lay["kq"], lay["ks"], lay["kz"]
-        v_q, v_scale, v_zero = lay["vq"], lay["vs"], lay["vz"]
         k_fp = v_fp = k_residual = v_residual = None
         head_dim = sh.d
         key_mode = "channel"
 
-    view = View()
+        def __init__(self, lay):
+            self.k_q, self.k_scale, self.k_zero = lay["kq"], lay["ks"], lay["kz"]
+            self.v_q, self.v_scale, self.v_zero = lay["vq"], lay["vs"], lay["vz"]
+
+    layers = []
+    for li in range(a.layers):
+        lay = packed_layout(sh.b, sh.hkv, sh.n, sh.d, device=dev)
+        shift = (li * 977) % sh.n
+        quantize_key_groups_into(torch.roll(kdev, shift, dims=2), lay["kq"], lay["ks"], lay["kz"], bits=4,
+                                 token_group=32)
+        quantize_values_into(torch.roll(vdev, shift, dims=2), lay["vq"], lay["vs"], lay["vz"], bits=4,
+                             channel_group=32)
+        prefix = Prefix(kq=lay["kq"], ks=lay["ks"], kz=lay["kz"], vq=lay["vq"], vs=lay["vs"], vz=lay["vz"],
+                        nq=sh.n, kb=4, vb=4)
+        compact_k = torch.empty((sh.b, sh.hkv, sh.read_k + sh.t, sh.d), dtype=torch.bfloat16, device=dev)
+        layers.append(dict(prefix=prefix, lay=lay, view=View(lay), ck=compact_k, cv=torch.empty_like(compact_k)))
+    del kdev, vdev
+    prefix, lay = layers[0]["prefix"], layers[0]["lay"]
     result = {}
 
-    def step():
-        out, stats = splitk_attention(qg, prefix, kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
-        mass, score = prefix_scores(qg, prefix, stats, rows, value=True)
+    def layer_step(L):
+        out, stats = splitk_attention(qg, L["prefix"], kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
+        mass, score = prefix_scores(qg, L["prefix"], stats, rows, value=True)
         idx = topk_ascending(score, sh.read_k)
-        gather_packed_kv(view, idx, out_key=compact_k[:, :, :sh.read_k], out_value=compact_v[:, :, :sh.read_k])
+        gather_packed_kv(L["view"], idx, out_key=L["ck"][:, :, :sh.read_k], out_value=L["cv"][:, :, :sh.read_k])
         result["out"], result["idx"] = out, idx
 
+    def step():
+        for L in layers:
+            layer_step(L)
+
     ms_step, _ = time_graph(step, a.steps, a.warmup)
+    ms_layer = ms_step / a.layers
 
     # The two large kernels of the step, each alone in its own graph of INNER launches
     # with the same arguments: split-K pass 1 and the value-aware score pass.
@@ -229,10 +249,10 @@ def main():
             step()
         e1.record()
         torch.cuda.synchronize()
-        ms_eager = e0.elapsed_time(e1) / a.steps
+        ms_eager = e0.elapsed_time(e1) / a.steps / a.layers
 
     alg = algorithmic(sh)
-    t_step = ms_step * 1e-3
+    t_step = ms_layer * 1e-3
     gbs = alg["bytes"] / t_step / 1e9
     kernels = {
         "splitk_partial": dict(kernel=PASS1_KERNEL, ms=ms_partial, flops=alg["pass1_flops"], bytes=alg["pass1_bytes"]),
@@ -259,7 +279,7 @@ def main():
         "metric": "\u00b5s per layer block-step + achieved HBM GB/s (% roofline), 32k prefix, int4 KV",
         "value": round(gbs, 2),
         "unit": "GB/s",
-        "us_per_layer_step": round(ms_step * 1e3, 3),
+        "us_per_layer_step": round(ms_layer * 1e3, 3),
         "hbm_roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
         "mfma_frac": round(alg["flops"] / t_step / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "n_gpus": 1,
@@ -272,7 +292,9 @@ def main():
         "dtype": "bf16 mfma / int4 kv",
         "data": "synthetic (seed 1234: N(0,1) Q/K/V, LogNormal(0,0.5) key channels, 4 sink keys x8)",
         "config": {"workload": f"{sh.name}: step 0 (split-K attention + value-aware scores + read-set top-k "
-                               f"+ gather), B{sh.b} Hq{sh.hq} Hkv{sh.hkv} D{sh.d} T{sh.t} read {sh.read_k}",
+                               f"+ gather), B{sh.b} Hq{sh.hq} Hkv{sh.hkv} D{sh.d} T{sh.t} read {sh.read_k}; "
+                               f"one step = {a.layers} layers, each with its own cache",
+                   "layers": a.layers,
                    "prefix": sh.n, "kv": "int4 k4v4 (KG 32, VG 32, f16 scale/zero)",
                    "split_tokens": a.split_tokens or "auto", "graph": True,
                    "algorithmic_bytes": alg["bytes"], "algorithmic_flops": alg["flops"]},
