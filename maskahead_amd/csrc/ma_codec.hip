@@ -115,8 +115,10 @@ __global__ void __launch_bounds__(256) dequant_prefix_kernel(PrefixArgs a, int H
 // ---------------------------------------------------------------- gather
 // grid (ceil(k / TPB_TOK), B*H), 256 threads; D/4 threads per selected entry, 4
 // channels each.  Indices outside [0, n) produce zeros (never an out-of-bounds read).
+// vec: the 4 key scales / zeros of a thread are one 8-byte load each and bf16 outputs are
+// written 8 bytes at a time (the host checks the alignment this needs).
 __global__ void __launch_bounds__(256) gather_kernel(PrefixArgs a, int H, int D, const int64_t *idx, int64_t sib,
-                                                     int64_t sih, int k, ma_tensor4 ko, ma_tensor4 vo) {
+                                                     int64_t sih, int k, ma_tensor4 ko, ma_tensor4 vo, int vec) {
     const int bh = blockIdx.y, b = bh / H, h = bh % H;
     const int tpt = D / 4;               // threads per token
     const int toks = 256 / tpt;
@@ -129,15 +131,35 @@ __global__ void __launch_bounds__(256) gather_kernel(PrefixArgs a, int H, int D,
     if (j64 >= 0 && j64 < n) {
         const int j = (int)j64;
         if (j < a.nq) {
+            const int g = j / KG, tt = j % KG;
+            const uint8_t *krow = a.kq + b * a.skq[0] + h * a.skq[1] + (int64_t)g * a.skq[2] + (int64_t)c0 * a.skq[3];
+            uint32_t kb[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) kx[e] = key_elem(a, b, h, j, c0 + e);
+            for (int e = 0; e < 4; ++e) kb[e] = krow[(int64_t)e * a.skq[3] + (tt >> 1)];
+            const int64_t so = b * a.sks[0] + h * a.sks[1] + (int64_t)g * a.sks[2] + c0;
+            uint16_t ks[4], kz[4];
+            if (vec) {
+                const uint2 sv = *(const uint2 *)&a.ks[so], zv = *(const uint2 *)&a.kz[so];
+                ks[0] = sv.x & 0xffffu; ks[1] = sv.x >> 16; ks[2] = sv.y & 0xffffu; ks[3] = sv.y >> 16;
+                kz[0] = zv.x & 0xffffu; kz[1] = zv.x >> 16; kz[2] = zv.y & 0xffffu; kz[3] = zv.y >> 16;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ks[e] = a.ks[so + e];
+                    kz[e] = a.kz[so + e];
+                }
+            }
             const int cg = c0 / VG, w = c0 % VG;
             const uint8_t *src = a.vq + b * a.svq[0] + h * a.svq[1] + (int64_t)j * a.svq[2] + (int64_t)cg * a.svq[3];
-            uint32_t two = (uint32_t)src[w >> 1] | ((uint32_t)src[(w >> 1) + 1] << 8);
-            int64_t so = b * a.svs[0] + h * a.svs[1] + (int64_t)j * a.svs[2] + cg;
-            float sc = ma_f16_to_f32(a.vs[so]), zp = ma_f16_to_f32(a.vz[so]);
+            const uint32_t two = (uint32_t)src[w >> 1] | ((uint32_t)src[(w >> 1) + 1] << 8);
+            const int64_t vso = b * a.svs[0] + h * a.svs[1] + (int64_t)j * a.svs[2] + cg;
+            const float vsc = ma_f16_to_f32(a.vs[vso]), vzp = ma_f16_to_f32(a.vz[vso]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) vx[e] = ma_dq((two >> (4 * e)) & 15u, sc, zp);
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t code = (tt & 1) ? (kb[e] >> 4) : (kb[e] & 15u);
+                kx[e] = ma_dq(code, ma_f16_to_f32(ks[e]), ma_f16_to_f32(kz[e]));
+                vx[e] = ma_dq((two >> (4 * e)) & 15u, vsc, vzp);
+            }
         } else {
             const int jf = j - a.nq;
 #pragma unroll
@@ -149,10 +171,20 @@ __global__ void __launch_bounds__(256) gather_kernel(PrefixArgs a, int H, int D,
     }
     const int64_t ok = b * ko.s[0] + h * ko.s[1] + (int64_t)i * ko.s[2] + c0;
     const int64_t ov = b * vo.s[0] + h * vo.s[1] + (int64_t)i * vo.s[2] + c0;
+    if (vec && ko.dtype == MA_BF16 && vo.dtype == MA_BF16) {
+        uint2 kw, vw;
+        kw.x = (uint32_t)ma_f32_to_bf16(kx[0]) | ((uint32_t)ma_f32_to_bf16(kx[1]) << 16);
+        kw.y = (uint32_t)ma_f32_to_bf16(kx[2]) | ((uint32_t)ma_f32_to_bf16(kx[3]) << 16);
+        vw.x = (uint32_t)ma_f32_to_bf16(vx[0]) | ((uint32_t)ma_f32_to_bf16(vx[1]) << 16);
+        vw.y = (uint32_t)ma_f32_to_bf16(vx[2]) | ((uint32_t)ma_f32_to_bf16(vx[3]) << 16);
+        *(uint2 *)((uint16_t *)ko.ptr + ok) = kw;
+        *(uint2 *)((uint16_t *)vo.ptr + ov) = vw;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        ma_store_f(ko.ptr, ok + e, ko.dtype, kx[e]);
-        ma_store_f(vo.ptr, ov + e, vo.dtype, vx[e]);
+        for (int e = 0; e < 4; ++e) {
+            ma_store_f(ko.ptr, ok + e, ko.dtype, kx[e]);
+            ma_store_f(vo.ptr, ov + e, vo.dtype, vx[e]);
+        }
     }
 }
 
@@ -327,8 +359,14 @@ extern "C" int ma_gather_kv(const ma_prefix *p, int B, int H, int D, const int64
     if (k == 0) return MA_OK;
     int toks = 256 / (D / 4);
     dim3 grid((k + toks - 1) / toks, B * H);
+    // 8-byte scale / zero loads and output stores: 8-byte aligned bases, strides in whole
+    // groups of 4 elements
+    auto al8 = [](const void *ptr) { return ((uintptr_t)ptr & 7) == 0; };
+    const int vec = al8(p->ks) && al8(p->kz) && p->sks[0] % 4 == 0 && p->sks[1] % 4 == 0 && p->sks[2] % 4 == 0 &&
+                    al8(k_out.ptr) && al8(v_out.ptr) && k_out.s[0] % 4 == 0 && k_out.s[1] % 4 == 0 &&
+                    k_out.s[2] % 4 == 0 && v_out.s[0] % 4 == 0 && v_out.s[1] % 4 == 0 && v_out.s[2] % 4 == 0;
     hipLaunchKernelGGL(gather_kernel, grid, dim3(256), 0, (hipStream_t)stream, make_args(p), H, D, idx, sidx[0],
-                       sidx[1], k, k_out, v_out);
+                       sidx[1], k, k_out, v_out, vec);
     return ma_check_launch("ma_gather_kv");
 }
 

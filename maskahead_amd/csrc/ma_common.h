@@ -163,6 +163,23 @@ __device__ __forceinline__ f32x16_t ma_mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// The 8 nibbles of a code word (nibble i = code of element i) as bytes: even nibbles
+// 0,2,4,6 in bytes 0..3 of `even`, odd nibbles 1,3,5,7 in bytes 0..3 of `odd`, so every
+// code converts to float with one v_cvt_f32_ubyteN (no per-code bit-field extract; the
+// compiler folds a plain shift-and-mask back into one, hence the explicit instruction).
+__device__ __forceinline__ void ma_nibble_bytes(uint32_t w, uint32_t &even, uint32_t &odd) {
+    even = w & 0x0f0f0f0fu;
+    odd = (w >> 4) & 0x0f0f0f0fu;
+}
+template <int K>
+__device__ __forceinline__ float ma_ubyte_f32(uint32_t x) {
+    float r;
+    if constexpr (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+    else if constexpr (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+    else if constexpr (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
 // ---- monotone float key for selection: larger float -> larger key; -0.0 == +0.0;
 // NaN above +inf (torch.topk ranks NaN first)
 __device__ __forceinline__ uint32_t ma_order_key(float f) {

@@ -82,12 +82,16 @@ __device__ __forceinline__ int sel_row(const int32_t *q_rows, int rr, int T2, in
 
 // 8 nibbles of a word as floats, element i = bits 4i..4i+3 (byte masks + cvt_f32_ubyte)
 __device__ __forceinline__ void nib8(uint32_t w, float *f) {
-    const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        f[2 * b] = (float)((lo >> (8 * b)) & 0xffu);
-        f[2 * b + 1] = (float)((hi >> (8 * b)) & 0xffu);
-    }
+    uint32_t lo, hi;
+    ma_nibble_bytes(w, lo, hi);
+    f[0] = ma_ubyte_f32<0>(lo);
+    f[1] = ma_ubyte_f32<0>(hi);
+    f[2] = ma_ubyte_f32<1>(lo);
+    f[3] = ma_ubyte_f32<1>(hi);
+    f[4] = ma_ubyte_f32<2>(lo);
+    f[5] = ma_ubyte_f32<2>(hi);
+    f[6] = ma_ubyte_f32<3>(lo);
+    f[7] = ma_ubyte_f32<3>(hi);
 }
 
 // K, packed: item u < 4D = (key group gl, 8-token quarter tq, channel pair dp), dp fastest

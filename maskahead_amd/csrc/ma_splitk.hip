@@ -11,9 +11,11 @@
 //                    register order the PV MFMA consumes, plus a per-row rescale factor.
 //   O waves 8..14    one tile behind: O^T = alpha * O^T + V^T P^T (A = V^T from LDS,
 //                    B = P^T from LDS); the accumulator keeps the lane's row.
-//   waves 7..15      staging: K lanes dequantize tile i+1 into the K buffer and prefetch
-//                    tile i+2; V lanes dequantize tile i into the V buffer and prefetch
-//                    tile i+1 (V is consumed one iteration later than K).
+//   waves 7..14      staging: K lanes (waves 7..10) dequantize tile i+1 into the K buffer
+//                    and prefetch tile i+2; V lanes (waves 11..14) dequantize tile i into
+//                    the V buffer and prefetch tile i+1 (V is consumed one iteration later
+//                    than K).  A wave holds lanes of one role only, so no wave executes
+//                    both staging paths.
 // K, V and P are double-buffered; every wave holds at most ~128 VGPRs, so the 16 waves
 // fit 4 per SIMD and the MFMA work of one wave overlaps the VALU work of the others.
 // Pass 2 (splitk_combine_kernel): log-sum-exp merge of the partials into the output and
@@ -28,8 +30,8 @@ namespace {
 
 constexpr int NTH = 1024;
 constexpr int MAXS = 7;                     // row tiles (S/O wave pairs) per workgroup
-constexpr int NSTAGE = 9 * 64;              // staging lanes: waves 7..15
-constexpr int KLANES = NSTAGE / 2;          // K lanes, then as many V lanes
+constexpr int NSTAGE = 8 * 64;              // staging lanes: waves 7..14 (wave 15 stages nothing)
+constexpr int KLANES = NSTAGE / 2;          // K lanes (waves 7..10), then as many V lanes (11..14)
 // a row's running reference max is raised only when a tile's max exceeds it by more than
 // 2^8 in exp2 units, so most tiles skip the accumulator rescale; p <= 2^8 stays exact
 constexpr float LAZY_LOG2 = 8.0f;
@@ -386,7 +388,7 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     // their registers for two tiles of S^T and the Q fragments
     const int st_lane = wave >= 7 ? tid - 7 * 64 : -1;
     const bool is_k = st_lane >= 0 && st_lane < KLANES;
-    const bool is_v = st_lane >= KLANES;
+    const bool is_v = st_lane >= KLANES && st_lane < NSTAGE;
     const int kl = st_lane, vl = st_lane - KLANES;
 
     auto tile_n0 = [&](int i) { return n_beg + i * TILE; };
@@ -402,8 +404,9 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
 
     StageRegs<Shape::NW> pr;
     pr.flags = 0;
-    // K lanes: global loads of tile i into pr; the dequant / copy into a K buffer
-    auto load_k = [&](int i) {
+    // K lanes: global loads of tile i into pr (or another register set); the dequant /
+    // copy into a K buffer
+    auto load_k_into = [&](StageRegs<Shape::NW> &pr, int i) {
         const int n0 = tile_n0(i);
         pr.flags = (kl < TILE && live(n0 + kl)) ? 256u : 0u;
         if constexpr (SRC == 0) {
@@ -417,7 +420,8 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         }
     };
-    auto store_k = [&](uint16_t *Ks, uint64_t &km) {
+    auto load_k = [&](int i) { load_k_into(pr, i); };
+    auto store_k_from = [&](StageRegs<Shape::NW> &pr, uint16_t *Ks, uint64_t &km) {
         if constexpr (SRC == 0) {
             if (kl < Shape::NK) store_k_packed<D>(Ks, pr.w, kl);
         } else {
@@ -432,6 +436,7 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             if (kl == 0) km = m;
         }
     };
+    auto store_k = [&](uint16_t *Ks, uint64_t &km) { store_k_from(pr, Ks, km); };
     // V lanes: global loads of tile i into pr; the dequant / copy into a V buffer
     auto load_v = [&](int i) {
         const int n0 = tile_n0(i);
@@ -523,16 +528,15 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         f32x16_t acc[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-        // prologue: K tiles 0 and 1 staged, K tile 2 and V tile 0 in flight
+        // prologue: K tiles 0 and 1 staged, K tile 2 and V tile 0 in flight (the loads of K
+        // tiles 0 and 1 are issued together, into two register sets)
         if (is_k) {
-            if (nt > 0) {
-                load_k(0);
-                store_k(S.kt[0].k, S.kmask[0]);
-            }
-            if (nt > 1) {
-                load_k(1);
-                store_k(S.kt[1].k, S.kmask[1]);
-            }
+            StageRegs<Shape::NW> pr1;
+            pr1.flags = 0;
+            if (nt > 0) load_k(0);
+            if (nt > 1) load_k_into(pr1, 1);
+            if (nt > 0) store_k(S.kt[0].k, S.kmask[0]);
+            if (nt > 1) store_k_from(pr1, S.kt[1].k, S.kmask[1]);
             if (nt > 2) load_k(2);
         } else if (is_v && nt > 0) {
             load_v(0);
@@ -558,16 +562,18 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     }
 }
 
-// Pass 2: grid (R, B*H), 128 threads = 8 split lanes x 16 channel octets.  The maximum
-// over the prefix splits first; then split lane sl sums splits sl, sl+8, ... with weights
-// l_s * exp(m_s - M), and the 8 lanes' sums are added in lane order through LDS, so the
-// result does not depend on timing.  Then the current block's partial joins.
+// Pass 2: grid (R, B*H), 128 threads = 8 split lanes x 16 channel octets.  Split lane
+// sl sums splits sl, sl+8, ... in order with weights l_s * exp(m_s - M); its loads for 8
+// splits (statistics and O) are issued together, the first batch before the maximum M over
+// the prefix splits is known.  The 8 lanes' sums are added in lane order through LDS, so
+// the result does not depend on timing.  Then the current block's partial joins.
 constexpr int CMB_SL = 8;
 
 template <int D>
 __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tensor4 out, float *mp_out, float *lp_out,
                                                              void *op_out) {
     constexpr int OCT = D / 8;
+    typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
     __shared__ float red[CMB_SL][D];
     __shared__ float lred[CMB_SL];
     __shared__ float smax[128 / 64];
@@ -575,6 +581,29 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
     const int tid = threadIdx.x;
     const int R = a.R, nsplit = a.nsplit;
     const int64_t base = (int64_t)bh * (nsplit + 1) * R + row;
+    const int sl = tid / OCT, oc = tid % OCT;
+    const bool lane_ok = sl < CMB_SL;
+    // one batch: splits i0 + u*8, u < 8, of this split lane
+    f16x8_t o[8];
+    float bm[8], bl[8], bs[8];
+    auto load_batch = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * CMB_SL;
+            bm[u] = -INFINITY;
+            bl[u] = 0.f;
+            bs[u] = 0.f;
+            o[u] = f16x8_t{};
+            if (lane_ok && i < nsplit) {
+                const int64_t pr = base + (int64_t)i * R;
+                bm[u] = a.wm[pr];
+                bl[u] = a.wl[pr];
+                bs[u] = a.wsc[pr];
+                o[u] = *(const f16x8_t *)&a.wo[pr * D + oc * 8];
+            }
+        }
+    };
+    load_batch(sl);
     // M = max over the prefix splits
     float m = -INFINITY;
     for (int sp = tid; sp < nsplit; sp += 128) m = fmaxf(m, a.wm[base + (int64_t)sp * R]);
@@ -583,21 +612,24 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
     __syncthreads();
     const float M = fmaxf(smax[0], smax[1]);
     const float msafe = M == -INFINITY ? 0.f : M;
-    const int sl = tid / OCT, oc = tid % OCT;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float lsum = 0.f;
-    if (sl < CMB_SL) {
-        for (int sp = sl; sp < nsplit; sp += CMB_SL) {
-            const int64_t pr = base + (int64_t)sp * R;
-            const float w = a.wl[pr] * expf(a.wm[pr] - msafe);
-            if (w == 0.f) continue;  // an empty split: its O is never read
-            const float ws = w * a.wsc[pr];
-            typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
-            const f16x8_t o = *(const f16x8_t *)&a.wo[pr * D + oc * 8];
+    for (int i0 = sl; lane_ok && i0 < nsplit;) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(ws, (float)o[e], acc[e]);
-            lsum += w;
+        for (int u = 0; u < 8; ++u) {
+            const int i = i0 + u * CMB_SL;
+            const float w = bl[u] * expf(bm[u] - msafe);
+            if (i < nsplit && w != 0.f) {   // an empty split (weight 0) adds nothing
+                const float ws = w * bs[u];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(ws, (float)o[u][e], acc[e]);
+                lsum += w;
+            }
         }
+        i0 += 8 * CMB_SL;
+        if (i0 < nsplit) load_batch(i0);
+    }
+    if (lane_ok) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) red[sl][oc * 8 + e] = acc[e];
         if (oc == 0) lred[sl] = lsum;

@@ -62,6 +62,28 @@ struct StageRegs {
     uint32_t flags;   // K lanes: bit 8 = this lane's token (lane < 64) usable; V lanes: bit 2i/2i+1 = tokens live
 };
 
+// element t (0..7) of a code word split by nibble_bytes, as float
+template <int T>
+__device__ __forceinline__ float code_f32(uint32_t even, uint32_t odd) {
+    return ma_ubyte_f32<T / 2>((T & 1) ? odd : even);
+}
+// the 8 dequantized elements of a code word, two code words (two channels or two tokens)
+// at a time, packed as bf16 pairs: out[t] = (element t of w0, element t of w1)
+__device__ __forceinline__ void dq8x2(uint32_t w0, uint32_t w1, float s0, float z0, float s1, float z1,
+                                      uint32_t (&out)[8]) {
+    uint32_t e0, o0, e1, o1;
+    ma_nibble_bytes(w0, e0, o0);
+    ma_nibble_bytes(w1, e1, o1);
+    out[0] = ma_pack_bf16x2(__builtin_fmaf(code_f32<0>(e0, o0), s0, z0), __builtin_fmaf(code_f32<0>(e1, o1), s1, z1));
+    out[1] = ma_pack_bf16x2(__builtin_fmaf(code_f32<1>(e0, o0), s0, z0), __builtin_fmaf(code_f32<1>(e1, o1), s1, z1));
+    out[2] = ma_pack_bf16x2(__builtin_fmaf(code_f32<2>(e0, o0), s0, z0), __builtin_fmaf(code_f32<2>(e1, o1), s1, z1));
+    out[3] = ma_pack_bf16x2(__builtin_fmaf(code_f32<3>(e0, o0), s0, z0), __builtin_fmaf(code_f32<3>(e1, o1), s1, z1));
+    out[4] = ma_pack_bf16x2(__builtin_fmaf(code_f32<4>(e0, o0), s0, z0), __builtin_fmaf(code_f32<4>(e1, o1), s1, z1));
+    out[5] = ma_pack_bf16x2(__builtin_fmaf(code_f32<5>(e0, o0), s0, z0), __builtin_fmaf(code_f32<5>(e1, o1), s1, z1));
+    out[6] = ma_pack_bf16x2(__builtin_fmaf(code_f32<6>(e0, o0), s0, z0), __builtin_fmaf(code_f32<6>(e1, o1), s1, z1));
+    out[7] = ma_pack_bf16x2(__builtin_fmaf(code_f32<7>(e0, o0), s0, z0), __builtin_fmaf(code_f32<7>(e1, o1), s1, z1));
+}
+
 // ------------------------------------------------------------------ packed K
 // item u: gl = u / D, th = (u / (D/2)) & 1, dp = u % (D/2)
 template <int D>
@@ -91,10 +113,11 @@ __device__ __forceinline__ void store_k_packed(uint16_t *Ks, const uint32_t *w, 
     const float z0 = ma_f16_to_f32(w[5] & 0xffff), z1 = ma_f16_to_f32(w[5] >> 16);
     uint32_t *dst = (uint32_t *)&Ks[(gl * KGRP + th * 16) * KS + 2 * dp];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        const uint32_t c0 = (w[t >> 3] >> ((t & 7) * 4)) & 15u;
-        const uint32_t c1 = (w[2 + (t >> 3)] >> ((t & 7) * 4)) & 15u;
-        dst[t * (KS / 2)] = ma_pack_bf16x2(ma_dq(c0, s0, z0), ma_dq(c1, s1, z1));
+    for (int q = 0; q < 2; ++q) {   // code word q: tokens 8q .. 8q+7 of the half
+        uint32_t pk[8];
+        dq8x2(w[q], w[2 + q], s0, z0, s1, z1, pk);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dst[(8 * q + t) * (KS / 2)] = pk[t];
     }
 }
 
@@ -129,10 +152,11 @@ __device__ __forceinline__ void store_v_packed(uint16_t *Vt, const uint32_t *w, 
     const float z0 = ma_f16_to_f32(w[5] & 0xffff), z1 = ma_f16_to_f32(w[5] >> 16);
     uint32_t *dst = (uint32_t *)&Vt[(cg * VGRP + ch * 16) * VS + vcol(2 * tp)];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-        const uint32_t c0 = (w[c >> 3] >> ((c & 7) * 4)) & 15u;
-        const uint32_t c1 = (w[2 + (c >> 3)] >> ((c & 7) * 4)) & 15u;
-        dst[c * (VS / 2)] = ma_pack_bf16x2(ma_dq(c0, s0, z0), ma_dq(c1, s1, z1));
+    for (int q = 0; q < 2; ++q) {   // code word q: channels 8q .. 8q+7 of the half
+        uint32_t pk[8];
+        dq8x2(w[q], w[2 + q], s0, z0, s1, z1, pk);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) dst[(8 * q + c) * (VS / 2)] = pk[c];
     }
 }
 
