@@ -437,8 +437,9 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         }
     };
     auto store_k = [&](uint16_t *Ks, uint64_t &km) { store_k_from(pr, Ks, km); };
-    // V lanes: global loads of tile i into pr; the dequant / copy into a V buffer
-    auto load_v = [&](int i) {
+    // V lanes: global loads of tile i into pr (or another register set); the dequant /
+    // copy into a V buffer
+    auto load_v_into = [&](StageRegs<Shape::NW> &pr, int i) {
         const int n0 = tile_n0(i);
         if constexpr (SRC == 0) {
             if (vl < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vl, n0, n_end);
@@ -455,7 +456,8 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         }
     };
-    auto store_v = [&](uint16_t *Vt) {
+    auto load_v = [&](int i) { load_v_into(pr, i); };
+    auto store_v_from = [&](StageRegs<Shape::NW> &pr, uint16_t *Vt) {
         if constexpr (SRC == 0) {
             if (vl < Shape::NV) store_v_packed<D>(Vt, pr.w, vl);
         } else {
@@ -466,6 +468,7 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         }
     };
+    auto store_v = [&](uint16_t *Vt) { store_v_from(pr, Vt); };
 
     const int qpos = a.q_pos0 + (row_ok ? row % a.T : 0);
     const bool causal = wk.cur && a.causal > 0;
@@ -486,8 +489,8 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
         }
         __syncthreads();  // prologue staging done
-        // Iteration it: the S waves issue S^T of tile it+1 (K is staged two tiles ahead)
-        // and, while those MFMAs run, do the softmax of tile it.  Tile masks travel with S^T.
+        // Iteration it: the S waves do the softmax of tile it and then issue S^T of tile it+1
+        // (K is staged two tiles ahead).  Tile masks travel with S^T.
         f32x16_t sa[2], sb[2];
         uint64_t ma = 0, mb = 0;
         if (is_s && nt > 0) {
@@ -495,18 +498,21 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             ma = S.kmask[0];
         }
         __syncthreads();  // K buffer 0 is read: the first iteration stages tile 2 into it
+        // The softmax of tile it (VALU) comes first and S^T of tile it+1 (MFMA) second: the
+        // O waves start a tile with their PV MFMAs and then stage (VALU), so the two kinds
+        // of waves keep the matrix pipe and the VALU busy at the same time.
         auto step = [&](int it, f32x16_t *sc, uint64_t mc, f32x16_t *sn, uint64_t &mn) {
             const int cb = it & 1;
-            if (is_s && it + 1 < nt) {
-                s_qk<D>(S.kt[cb ^ 1].k, qf, c32, hf, sn);
-                mn = S.kmask[cb ^ 1];
-            }
             if (is_s && it < nt) {
                 const int n0 = tile_n0(it);
                 const int lim = causal ? (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4 : TILE;
                 const bool need_mask = causal || mc != ~0ull;
                 s_softmax<D>(sc, mc, m_ref, m_true, l, c32, hf, lane, need_mask, lim, a.sl2, &S.p[cb][rw][0][0],
                              S.alpha[cb][rw], &S.resc[cb][rw]);
+            }
+            if (is_s && it + 1 < nt) {
+                s_qk<D>(S.kt[cb ^ 1].k, qf, c32, hf, sn);
+                mn = S.kmask[cb ^ 1];
             }
             __syncthreads();
         };
@@ -528,33 +534,49 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         f32x16_t acc[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-        // prologue: K tiles 0 and 1 staged, K tile 2 and V tile 0 in flight (the loads of K
-        // tiles 0 and 1 are issued together, into two register sets)
+        // Staging lanes hold two register sets (tile t in set t & 1) when the source is
+        // packed, so a tile's global loads are issued two iterations before its dequant:
+        // K lanes load tile it+4 while staging tile it+2, V lanes tile it+2 while staging
+        // tile it.  (16-bit sources need more registers per set: one set, one iteration.)
+        constexpr bool DEEP = SRC == 0;
+        StageRegs<Shape::NW> prb;
+        prb.flags = 0;
+        // prologue: K tiles 0 and 1 staged, K tiles 2 (and 3) and V tile 0 (and 1) in flight
         if (is_k) {
-            StageRegs<Shape::NW> pr1;
-            pr1.flags = 0;
             if (nt > 0) load_k(0);
-            if (nt > 1) load_k_into(pr1, 1);
+            if (nt > 1) load_k_into(prb, 1);
             if (nt > 0) store_k(S.kt[0].k, S.kmask[0]);
-            if (nt > 1) store_k_from(pr1, S.kt[1].k, S.kmask[1]);
+            if (nt > 1) store_k_from(prb, S.kt[1].k, S.kmask[1]);
             if (nt > 2) load_k(2);
-        } else if (is_v && nt > 0) {
-            load_v(0);
+            if (DEEP && nt > 3) load_k_into(prb, 3);
+        } else if (is_v) {
+            if (nt > 0) load_v(0);
+            if (DEEP && nt > 1) load_v_into(prb, 1);
         }
         __syncthreads();
         __syncthreads();  // the S waves have read K tile 0 out of buffer 0
-        for (int it = 0; it <= nt; ++it) {
+        auto body = [&](int it, StageRegs<Shape::NW> &set) {
             const int cb = it & 1, pb = cb ^ 1;
             if (is_o && it >= 1)
                 o_tile<D>(S.vt[pb].vt, &S.p[pb][rw][0][0], S.alpha[pb][rw], S.resc[pb][rw], acc, c32, hf, lane);
             if (is_k && it + 2 < nt) {
-                store_k(S.kt[cb].k, S.kmask[cb]);
-                if (it + 3 < nt) load_k(it + 3);
+                store_k_from(set, S.kt[cb].k, S.kmask[cb]);
+                if (it + (DEEP ? 4 : 3) < nt) load_k_into(set, it + (DEEP ? 4 : 3));
             } else if (is_v && it < nt) {
-                store_v(S.vt[cb].vt);
-                if (it + 1 < nt) load_v(it + 1);
+                store_v_from(set, S.vt[cb].vt);
+                if (it + (DEEP ? 2 : 1) < nt) load_v_into(set, it + (DEEP ? 2 : 1));
             }
             __syncthreads();
+        };
+        if constexpr (DEEP) {
+            int it = 0;
+            for (; it + 1 <= nt; it += 2) {
+                body(it, pr);
+                body(it + 1, prb);
+            }
+            if (it <= nt) body(it, pr);
+        } else {
+            for (int it = 0; it <= nt; ++it) body(it, pr);
         }
         __syncthreads();  // final statistics of the S waves
         if (is_o && row_ok)
