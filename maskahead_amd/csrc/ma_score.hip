@@ -274,6 +274,8 @@ struct ScoreSmem {
     int rrow[MAX_R2];           // per selection row: its row in [0, R)
     int qoff[MAX_R2];           // per selection row: element offset of its query from (b, h*G, 0)
     int cnt[MAX_R];             // per row r < R: how many selection rows it is
+    float rowc[MAX_R];          // per row r < R: M_p*log2e + log2(L_p), +inf when L_p = 0
+    int qr[MAX_R2];             // q_rows (T2 <= MAX_R2 entries)
 };
 
 // Every wave does both jobs, in lock step: S units (a 32-row tile x a 32-token half of a
@@ -350,9 +352,16 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
         }
     };
 
-    // ---- prologue: the first tile's loads, then the selection-row tables (one load per
-    // row), then Q and the value centre
+    // ---- prologue: the first tile's loads, q_rows and M_p / L_p of every row at once, then
+    // the selection-row tables from LDS, then Q and the value centre
     if (fast) load(0);
+    if (tid < T2) sm.qr[tid] = a.q_rows[tid];
+    for (int r = tid; r < R; r += SNT) {
+        const float m = a.mp[(int64_t)bh * R + r], l = a.lp[(int64_t)bh * R + r];
+        // exp(s - M) / L == exp2(s*log2e - (M*log2e + log2 L)); rows without a live prefix
+        // entry (L = 0) and padding rows contribute exactly 0
+        sm.rowc[r] = l > 0.f ? __builtin_fmaf(m, MA_LOG2E, __log2f(l)) : __builtin_inff();
+    }
     for (int r = tid; r < MAX_R; r += SNT) sm.cnt[r] = 0;
     __syncthreads();
     const int rt_pad = 32 * row_tiles;
@@ -360,14 +369,12 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
         float c = __builtin_inff();
         int row = 0, qo = -1;
         if (rr < R2) {
-            int g, t;
-            row = sel_row(a.q_rows, rr, T2, T, &g, &t);
+            const int g = rr / T2;
+            const int t = min(max(sm.qr[rr - g * T2], 0), T - 1);   // as sel_row
+            row = g * T + t;
             qo = g * (int)a.q.s[1] + t * (int)a.q.s[2];
             atomicAdd(&sm.cnt[row], 1);
-            const float m = a.mp[(int64_t)bh * R + row], l = a.lp[(int64_t)bh * R + row];
-            // exp(s - M) / L == exp2(s*log2e - (M*log2e + log2 L)); rows without a live
-            // prefix entry (L = 0) and padding rows contribute exactly 0
-            if (l > 0.f) c = __builtin_fmaf(m, MA_LOG2E, __log2f(l));
+            c = sm.rowc[row];
         }
         sm.crow[rr] = c;
         sm.rrow[rr] = row;

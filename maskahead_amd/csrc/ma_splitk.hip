@@ -626,6 +626,15 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
         }
     };
     load_batch(sl);
+    // the current block's partial (slot nsplit), needed after the reduction
+    const int64_t pc = base + (int64_t)nsplit * R;
+    float mc = -INFINITY, lc = 0.f, oc_raw = 0.f, sc_c = 0.f;
+    if (tid < D) {
+        mc = a.wm[pc];
+        lc = a.wl[pc];
+        oc_raw = (float)a.wo[pc * D + tid];
+        sc_c = a.wsc[pc];
+    }
     // M = max over the prefix splits
     float m = -INFINITY;
     for (int sp = tid; sp < nsplit; sp += 128) m = fmaxf(m, a.wm[base + (int64_t)sp * R]);
@@ -666,9 +675,7 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
         lp += lred[k];
     }
     // current block (slot nsplit)
-    const int64_t pc = base + (int64_t)nsplit * R;
-    const float mc = a.wm[pc], lc = a.wl[pc];
-    const float oc_d = lc > 0.f ? (float)a.wo[pc * D + d] * a.wsc[pc] : 0.f;
+    const float oc_d = lc > 0.f ? oc_raw * sc_c : 0.f;
     const float mm = fmaxf(M, mc);
     const float ms = (mm == -INFINITY) ? 0.f : mm;
     const float ea = expf(M - ms), eb = expf(mc - ms);
