@@ -406,8 +406,26 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     pr.flags = 0;
     // K lanes: global loads of tile i into pr (or another register set); the dequant /
     // copy into a K buffer
+    // packed whole tiles: this lane's item offsets, once
+    uint2 item_off = uint2{0u, 0u};
+    if constexpr (SRC == 0) {
+        if (is_k && kl < Shape::NK) item_off = k_item_offsets<D>(L, kl);
+        else if (is_v && vl < Shape::NV) item_off = v_item_offsets<D>(L, vl);
+    }
+    const bool fast_tiles = SRC == 0 && !L.mask;   // whole tiles of an unmasked packed prefix
     auto load_k_into = [&](StageRegs<Shape::NW> &pr, int i) {
         const int n0 = tile_n0(i);
+        if constexpr (SRC == 0) {
+            if (fast_tiles && n0 + TILE <= n_end) {
+                pr.flags = kl < TILE ? 256u : 0u;
+                if (kl < Shape::NK) {
+                    const int64_t g0 = n0 / KGRP;
+                    load_k_packed_fast(pr.w, L.kq + g0 * L.kq_g, L.ks + g0 * L.ks_g, L.kz + g0 * L.ks_g, L.kq_d,
+                                       item_off);
+                }
+                return;
+            }
+        }
         pr.flags = (kl < TILE && live(n0 + kl)) ? 256u : 0u;
         if constexpr (SRC == 0) {
             if (kl < Shape::NK) load_k_packed<D>(pr.w, L, kl, n0, n_end);
@@ -442,6 +460,14 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     auto load_v_into = [&](StageRegs<Shape::NW> &pr, int i) {
         const int n0 = tile_n0(i);
         if constexpr (SRC == 0) {
+            if (fast_tiles && n0 + TILE <= n_end) {
+                if (vl < Shape::NV) {
+                    load_v_packed_fast(pr.w, L.vq + (int64_t)n0 * L.vq_n, L.vs + (int64_t)n0 * L.vs_n,
+                                       L.vz + (int64_t)n0 * L.vs_n, L.vq_n, L.vs_n, item_off);
+                    pr.flags = 3u;
+                }
+                return;
+            }
             if (vl < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vl, n0, n_end);
         } else {
             const char *base = ds.v + (int64_t)(n0 - ds.tok0) * ds.sv * ds.esz;
@@ -534,49 +560,33 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         f32x16_t acc[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-        // Staging lanes hold two register sets (tile t in set t & 1) when the source is
-        // packed, so a tile's global loads are issued two iterations before its dequant:
-        // K lanes load tile it+4 while staging tile it+2, V lanes tile it+2 while staging
-        // tile it.  (16-bit sources need more registers per set: one set, one iteration.)
-        constexpr bool DEEP = SRC == 0;
-        StageRegs<Shape::NW> prb;
-        prb.flags = 0;
-        // prologue: K tiles 0 and 1 staged, K tiles 2 (and 3) and V tile 0 (and 1) in flight
+        // prologue: K tiles 0 and 1 staged (their loads issued together, into two register
+        // sets), K tile 2 and V tile 0 in flight
         if (is_k) {
+            StageRegs<Shape::NW> pr1;
+            pr1.flags = 0;
             if (nt > 0) load_k(0);
-            if (nt > 1) load_k_into(prb, 1);
+            if (nt > 1) load_k_into(pr1, 1);
             if (nt > 0) store_k(S.kt[0].k, S.kmask[0]);
-            if (nt > 1) store_k_from(prb, S.kt[1].k, S.kmask[1]);
+            if (nt > 1) store_k_from(pr1, S.kt[1].k, S.kmask[1]);
             if (nt > 2) load_k(2);
-            if (DEEP && nt > 3) load_k_into(prb, 3);
-        } else if (is_v) {
-            if (nt > 0) load_v(0);
-            if (DEEP && nt > 1) load_v_into(prb, 1);
+        } else if (is_v && nt > 0) {
+            load_v(0);
         }
         __syncthreads();
         __syncthreads();  // the S waves have read K tile 0 out of buffer 0
-        auto body = [&](int it, StageRegs<Shape::NW> &set) {
+        for (int it = 0; it <= nt; ++it) {
             const int cb = it & 1, pb = cb ^ 1;
             if (is_o && it >= 1)
                 o_tile<D>(S.vt[pb].vt, &S.p[pb][rw][0][0], S.alpha[pb][rw], S.resc[pb][rw], acc, c32, hf, lane);
             if (is_k && it + 2 < nt) {
-                store_k_from(set, S.kt[cb].k, S.kmask[cb]);
-                if (it + (DEEP ? 4 : 3) < nt) load_k_into(set, it + (DEEP ? 4 : 3));
+                store_k(S.kt[cb].k, S.kmask[cb]);
+                if (it + 3 < nt) load_k(it + 3);
             } else if (is_v && it < nt) {
-                store_v_from(set, S.vt[cb].vt);
-                if (it + (DEEP ? 2 : 1) < nt) load_v_into(set, it + (DEEP ? 2 : 1));
+                store_v(S.vt[cb].vt);
+                if (it + 1 < nt) load_v(it + 1);
             }
             __syncthreads();
-        };
-        if constexpr (DEEP) {
-            int it = 0;
-            for (; it + 1 <= nt; it += 2) {
-                body(it, pr);
-                body(it + 1, prb);
-            }
-            if (it <= nt) body(it, pr);
-        } else {
-            for (int it = 0; it <= nt; ++it) body(it, pr);
         }
         __syncthreads();  // final statistics of the S waves
         if (is_o && row_ok)

@@ -121,6 +121,27 @@ __device__ __forceinline__ void store_k_packed(uint16_t *Ks, const uint32_t *w, 
     }
 }
 
+// Whole-tile fast path (a full 64-token tile of packed groups, no slot mask): an item's
+// offsets from the tile's first key group are fixed per lane, so a tile moves only the
+// wave-uniform base pointers (no per-tile 64-bit index arithmetic, clamps or liveness).
+template <int D>
+__device__ __forceinline__ uint2 k_item_offsets(const Lane &L, int u) {
+    const int dp = u % (D / 2), th = (u / (D / 2)) & 1, gl = u / D;
+    return uint2{(uint32_t)(gl * L.kq_g + 2 * dp * L.kq_d + th * 8), (uint32_t)(gl * L.ks_g + 2 * dp)};
+}
+// the words of load_k_packed for the tile whose first key group starts at kq / ks / kz
+__device__ __forceinline__ void load_k_packed_fast(uint32_t *w, const uint8_t *kq, const uint16_t *ks,
+                                                   const uint16_t *kz, int kq_d, uint2 o) {
+    const uint2 x0 = *(const uint2 *)(kq + o.x);
+    const uint2 x1 = *(const uint2 *)(kq + o.x + kq_d);
+    w[0] = x0.x;
+    w[1] = x0.y;
+    w[2] = x1.x;
+    w[3] = x1.y;
+    w[4] = *(const uint32_t *)(ks + o.y);
+    w[5] = *(const uint32_t *)(kz + o.y);
+}
+
 // ------------------------------------------------------------------ packed V
 // item u: tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6; tokens 2tp, 2tp+1
 template <int D>
@@ -142,6 +163,25 @@ __device__ __forceinline__ void load_v_packed(uint32_t *w, uint32_t &flags, cons
     w[4] = (l0 ? s0 : 0u) | ((l1 ? s1 : 0u) << 16);
     w[5] = (l0 ? z0 : 0u) | ((l1 ? z1 : 0u) << 16);
     flags = (l0 ? 1u : 0u) | (l1 ? 2u : 0u);
+}
+
+// whole-tile fast path of load_v_packed (both tokens live)
+template <int D>
+__device__ __forceinline__ uint2 v_item_offsets(const Lane &L, int u) {
+    const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
+    return uint2{(uint32_t)(2 * tp * L.vq_n + cg * L.vq_c + ch * 8), (uint32_t)(2 * tp * L.vs_n + cg)};
+}
+__device__ __forceinline__ void load_v_packed_fast(uint32_t *w, const uint8_t *vq, const uint16_t *vs,
+                                                   const uint16_t *vz, int vq_n, int vs_n, uint2 o) {
+    const uint2 x0 = *(const uint2 *)(vq + o.x);
+    const uint2 x1 = *(const uint2 *)(vq + o.x + vq_n);
+    const uint32_t s0 = vs[o.y], z0 = vz[o.y], s1 = vs[o.y + vs_n], z1 = vz[o.y + vs_n];
+    w[0] = x0.x;
+    w[1] = x0.y;
+    w[2] = x1.x;
+    w[3] = x1.y;
+    w[4] = s0 | (s1 << 16);
+    w[5] = z0 | (z1 << 16);
 }
 
 template <int D>
