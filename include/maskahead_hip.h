@@ -155,11 +155,14 @@ int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, 
  * Positions (int32, or int64 when pos_is_i64) must increase strictly along each row --
  * the state keeps its live arrays in position order -- so index order is position order
  * and the newest W are the last W; status (optional, int32 [rows]) gets 1 for a row that
- * breaks this.  pin_lo_rows (optional, [rows]) overrides pin_lo per row. */
+ * breaks this.  pin_lo_rows (optional, [rows]) overrides pin_lo per row.  n <= 4M.  The
+ * selection runs as ma_topk_select's three launches, with the same state buffer
+ * (ma_topk_state_bytes(rows)) and workspace (ma_topk_workspace_bytes(rows, n)). */
 int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const float *score,
                    int64_t score_stride, int rows, int n, int capacity, int window, int64_t sink_tokens,
                    const int64_t *pin_lo_rows, int64_t pin_lo, int64_t pin_hi, int has_pin, int64_t *keep,
-                   int64_t keep_stride, int32_t *status, void *stream);
+                   int64_t keep_stride, int32_t *status, void *state, int64_t state_bytes, void *workspace,
+                   int64_t workspace_bytes, void *stream);
 
 /* a8. value_score (session.py:27-40): score[row, j] = a[row, j] * ||v_j - c||,
  * c = sum_j w_j v_j / max(sum_j w_j, 1e-12), rows = (b, h) of v [B,H,n,D] (strides b, h, n;

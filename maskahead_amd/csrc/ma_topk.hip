@@ -1,6 +1,13 @@
-// Read-set top-k over many workgroups per row (session.py:1429-1438,
-// reference.py:369-393): rank.masked_fill(dead, -inf).topk(k) with its indices sorted,
-// ties at the k-th value going to the smaller index.
+// Per-row selection over many workgroups per row, ties at the k-th value going to the
+// smaller index:
+//   * read set (session.py:1429-1438, reference.py:369-393):
+//     rank.masked_fill(dead, -inf).topk(k) with its indices sorted;
+//   * keep set (EvictionState.survivors, eviction.py:325-409, score-ranked policies): the
+//     W = min(window, C) newest entries plus the top (C - W) of the score among the others,
+//     positions < sink_tokens and pinned positions ranking +inf, in position order.  The
+//     state keeps a lane's live entries in position order, so the newest W are the last W,
+//     the contest runs over the first m = n - W entries as a top-(C - W), and index order
+//     is position order; a row whose positions do not increase strictly gets status 1.
 //
 // A row is cut into C chunks of CS = 256 * VPT elements; workgroup (c, row) owns chunk c
 // in all three kernels, so a chunk is re-read from the L2 of the XCD that read it first.
@@ -46,7 +53,7 @@ struct alignas(256) RowState {
     uint32_t hist[H0];   // zero between calls
 };
 struct ChunkInfo {
-    uint32_t gt;      // keys of the chunk above bin d0
+    uint32_t gt;      // keys of the chunk above bin d0; bit 31: positions out of order (keep)
     uint32_t ncand;   // keys of the chunk in bin d0 (its candidates)
     uint32_t d0;      // the row's boundary bin and
     uint32_t krem;    // how many of its keys are selected
@@ -64,6 +71,13 @@ struct TopkArgs {
     RowState *state;     // [rows]
     ChunkInfo *chunk;    // [rows][C]
     uint2 *cand;         // [rows][C][CS]: (key, index) per chunk
+    // keep set: positions (int32 or int64) and the sink / pin rules; keys of entries j >= m
+    // (the W newest) are 0, so they never contest and are appended after the selection
+    const void *pos;
+    int pos_i64, m, w, has_pin;
+    int64_t pos_stride, sink, pin_lo, pin_hi;
+    const int64_t *pin_lo_rows;
+    int32_t *status;
 };
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
@@ -76,11 +90,23 @@ __device__ __forceinline__ int chunk_index(int c, int e) {
     return c * (TB * VPT) + 4 * ((e >> 2) * TB + (int)threadIdx.x) + (e & 3);
 }
 
-// keys of this thread's elements; 0 (below every real key) past the end of the row
-template <int VPT>
-__device__ __forceinline__ void chunk_keys(const TopkArgs &a, int row, int c, uint32_t (&key)[VPT]) {
+__device__ __forceinline__ int64_t pos_at(const TopkArgs &a, int64_t off) {
+    return a.pos_i64 ? ((const int64_t *)a.pos)[off] : (int64_t)((const int32_t *)a.pos)[off];
+}
+
+// keys of this thread's elements; 0 (below every real key) past the end of the row.  KEEP:
+// the keep-set keys (sinks and pinned positions +inf, entries j >= m 0) and, in *bad, the
+// order check of the thread's elements against their predecessors.
+template <int VPT, bool KEEP>
+__device__ __forceinline__ void chunk_keys(const TopkArgs &a, int row, int c, uint32_t (&key)[VPT],
+                                           bool *bad = nullptr) {
     const float *rr = a.rank + (int64_t)row * a.rank_stride;
     const uint8_t *mr = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
+    int64_t plo = 0, prow = 0;
+    if constexpr (KEEP) {
+        plo = a.pin_lo_rows ? a.pin_lo_rows[row] : a.pin_lo;
+        prow = (int64_t)row * a.pos_stride;
+    }
 #pragma unroll
     for (int q = 0; q < VPT / 4; ++q) {
         const int j0 = chunk_index<VPT>(c, 4 * q);
@@ -95,11 +121,27 @@ __device__ __forceinline__ void chunk_keys(const TopkArgs &a, int row, int c, ui
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = j0 + i < a.n ? rr[j0 + i] : 0.f;
         }
+        if constexpr (KEEP) {
+            int64_t p[5];   // the run's positions and its predecessor's (clamped indices)
+            p[0] = pos_at(a, prow + min(max(j0 - 1, 0), a.n - 1));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = j0 + i;
-            const bool live = !mr || (j < a.n && mr[j] != 0);
-            key[4 * q + i] = j < a.n ? ma_order_key(live ? v[i] : -INFINITY) : 0u;
+            for (int i = 0; i < 4; ++i) p[i + 1] = pos_at(a, prow + min(j0 + i, a.n - 1));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = j0 + i;
+                if (bad) *bad |= (j > 0 && j < a.n) && !(p[i] < p[i + 1]);
+                float x = v[i];
+                if (p[i + 1] < a.sink) x = INFINITY;
+                if (a.has_pin && p[i + 1] >= plo && p[i + 1] < a.pin_hi) x = INFINITY;
+                key[4 * q + i] = j < a.m ? ma_order_key(x) : 0u;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = j0 + i;
+                const bool live = !mr || (j < a.n && mr[j] != 0);
+                key[4 * q + i] = j < a.n ? ma_order_key(live ? v[i] : -INFINITY) : 0u;
+            }
         }
     }
 }
@@ -176,13 +218,13 @@ __device__ __forceinline__ void find_digit(const uint32_t (&h)[PB], uint32_t kk,
 }
 
 // Level-0 histogram of the chunk added into the row's histogram.
-template <int VPT>
+template <int VPT, bool KEEP>
 __global__ void __launch_bounds__(TB) topk_hist_kernel(TopkArgs a) {
     __shared__ uint32_t h[H0];
     const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     for (int i = tid; i < H0 / 4; i += TB) ((uint4 *)h)[i] = make_uint4(0u, 0u, 0u, 0u);
     uint32_t key[VPT];
-    chunk_keys<VPT>(a, row, c, key);
+    chunk_keys<VPT, KEEP>(a, row, c, key);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < VPT; ++e)
@@ -196,7 +238,7 @@ __global__ void __launch_bounds__(TB) topk_hist_kernel(TopkArgs a) {
 }
 
 // d0 / krem from the row's histogram; the chunk's count above bin d0 and its candidates.
-template <int VPT>
+template <int VPT, bool KEEP>
 __global__ void __launch_bounds__(TB) topk_boundary_kernel(TopkArgs a) {
     constexpr int CS = TB * VPT, PB = H0 / TB;
     __shared__ uint32_t wsum[TW], found[2];
@@ -213,7 +255,8 @@ __global__ void __launch_bounds__(TB) topk_boundary_kernel(TopkArgs a) {
         cnt[4 * i + 3] = x.w;
     }
     uint32_t key[VPT];
-    chunk_keys<VPT>(a, row, c, key);
+    bool bad = false;
+    chunk_keys<VPT, KEEP>(a, row, c, key, &bad);
     find_digit<PB>(cnt, (uint32_t)a.k, wsum, found);
     const uint32_t d0 = found[0], krem = (uint32_t)a.k - found[1];
     uint32_t packed[1] = {0u};   // low 16 bits: keys above bin d0; high: keys in bin d0
@@ -233,9 +276,10 @@ __global__ void __launch_bounds__(TB) topk_boundary_kernel(TopkArgs a) {
             ++pos;
         }
     }
+    const bool chunk_bad = KEEP && __syncthreads_or(bad);
     if (tid == 0) {
         ChunkInfo ci;
-        ci.gt = total & 0xffffu;
+        ci.gt = (total & 0xffffu) | (chunk_bad ? 0x80000000u : 0u);
         ci.ncand = total >> 16;
         ci.d0 = d0;
         ci.krem = krem;
@@ -254,7 +298,7 @@ struct EmitSmem {
 
 // T, need and the chunk's base from the row's candidates; the chunk's selected indices,
 // ascending, to idx[base ..]; values optional.
-template <int VPT>
+template <int VPT, bool KEEP>
 __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
     constexpr int NR = VPT / 4, CS = TB * VPT;
     __shared__ EmitSmem S;
@@ -263,6 +307,7 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
     const ChunkInfo *info = a.chunk + (int64_t)row * C;
     // chunk records of chunks [4t, 4t + 4) and the chunk's keys, loads in flight together
     uint32_t gt[4], nc[4];
+    bool any_bad = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int ch = 4 * tid + i;
@@ -270,13 +315,24 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
         nc[i] = 0u;
         if (ch < C) {
             const ChunkInfo x = info[ch];
-            gt[i] = x.gt;
+            any_bad |= (x.gt >> 31) != 0u;
+            gt[i] = x.gt & 0x7fffffffu;
             nc[i] = x.ncand;
         }
     }
     const uint32_t d0 = info[0].d0, krem = info[0].krem;
     uint32_t key[VPT];
-    chunk_keys<VPT>(a, row, c, key);
+    chunk_keys<VPT, KEEP>(a, row, c, key);
+    if constexpr (KEEP) {
+        // workgroup 0 of the row: the order flag of the row and the W newest entries after
+        // the selected ones
+        const bool row_bad = __syncthreads_or(any_bad);
+        if (c == 0) {
+            if (tid == 0 && a.status) a.status[row] = row_bad ? 1 : 0;
+            int64_t *wout = a.idx + (int64_t)row * a.idx_stride + a.k;
+            for (int i = tid; i < a.w; i += TB) wout[i] = (int64_t)(a.m + i);
+        }
+    }
     uint32_t run[1] = {nc[0] + nc[1] + nc[2] + nc[3]};
     const uint32_t NC = block_prefix_runs<1>(run, S.wsum);
     {
@@ -489,6 +545,58 @@ extern "C" int64_t ma_topk_workspace_bytes(int rows, int n) {
     return chunk_bytes(rows, n) + align256((int64_t)rows * C * TB * vpt * (int64_t)sizeof(uint2));
 }
 
+namespace {
+
+// shared argument checks and fill of both entry points (rank = the score row, k = the
+// number to select); MA_OK with rows == 0 or k == 0 and no keep window means nothing to do
+int topk_prepare(TopkArgs &a, int &vpt, const char *who, const float *rank, int64_t rank_stride, int rows, int n,
+                 int k, int64_t *idx, int64_t idx_stride, void *state, int64_t state_bytes, void *workspace,
+                 int64_t workspace_bytes) {
+    vpt = topk_vpt(n);
+    if (!vpt) {
+        ma_set_error("%s: n=%d exceeds the built maximum %d", who, n, TB * 16 * MAX_CHUNKS);
+        return MA_EUNSUPPORTED;
+    }
+    const int64_t need_state = ma_topk_state_bytes(rows), need_ws = ma_topk_workspace_bytes(rows, n);
+    if (!state || state_bytes < need_state || ((uintptr_t)state & 255) || !workspace ||
+        workspace_bytes < need_ws || ((uintptr_t)workspace & 255)) {
+        ma_set_error("%s: state of %lld and workspace of %lld bytes (256-byte aligned) needed, got %lld and %lld",
+                     who, (long long)need_state, (long long)need_ws, (long long)state_bytes,
+                     (long long)workspace_bytes);
+        return MA_EINVAL;
+    }
+    a = TopkArgs{};
+    a.rank = rank;
+    a.rank_stride = rank_stride;
+    a.n = n;
+    a.k = k;
+    a.C = (n + TB * vpt - 1) / (TB * vpt);
+    a.vec = ((uintptr_t)rank & 15) == 0 && rank_stride % 4 == 0;
+    a.idx = idx;
+    a.idx_stride = idx_stride;
+    a.state = (RowState *)state;
+    a.chunk = (ChunkInfo *)workspace;
+    a.cand = (uint2 *)((char *)workspace + chunk_bytes(rows, n));
+    return MA_OK;
+}
+
+template <bool KEEP>
+int topk_launch(const TopkArgs &a, int rows, int vpt, hipStream_t st, const char *who) {
+    const dim3 grid(a.C, rows);
+    if (vpt == 4) {
+        hipLaunchKernelGGL((topk_hist_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL((topk_boundary_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL((topk_emit_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((topk_hist_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL((topk_boundary_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
+        hipLaunchKernelGGL((topk_emit_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
+    }
+    return ma_check_launch(who);
+}
+
+}  // namespace
+
 extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, int64_t mask_stride,
                               int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values,
                               void *state, int64_t state_bytes, void *workspace, int64_t workspace_bytes,
@@ -499,44 +607,45 @@ extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint
         return MA_EINVAL;
     }
     if (rows == 0 || k == 0) return MA_OK;
-    const int vpt = topk_vpt(n);
-    if (!vpt) {
-        ma_set_error("ma_topk_select: n=%d exceeds the built maximum %d", n, TB * 16 * MAX_CHUNKS);
-        return MA_EUNSUPPORTED;
-    }
-    const int64_t need_state = ma_topk_state_bytes(rows), need_ws = ma_topk_workspace_bytes(rows, n);
-    if (!state || state_bytes < need_state || ((uintptr_t)state & 255) || !workspace ||
-        workspace_bytes < need_ws || ((uintptr_t)workspace & 255)) {
-        ma_set_error("ma_topk_select: state of %lld and workspace of %lld bytes (256-byte aligned) needed, "
-                     "got %lld and %lld", (long long)need_state, (long long)need_ws, (long long)state_bytes,
-                     (long long)workspace_bytes);
-        return MA_EINVAL;
-    }
     TopkArgs a;
-    a.rank = rank;
-    a.rank_stride = rank_stride;
+    int vpt = 0;
+    const int rc = topk_prepare(a, vpt, "ma_topk_select", rank, rank_stride, rows, n, k, idx, idx_stride, state,
+                                state_bytes, workspace, workspace_bytes);
+    if (rc) return rc;
     a.mask = mask;
     a.mask_stride = mask_stride;
-    a.n = n;
-    a.k = k;
-    a.C = (n + TB * vpt - 1) / (TB * vpt);
-    a.vec = ((uintptr_t)rank & 15) == 0 && rank_stride % 4 == 0;
-    a.idx = idx;
-    a.idx_stride = idx_stride;
     a.values = values;
-    a.state = (RowState *)state;
-    a.chunk = (ChunkInfo *)workspace;
-    a.cand = (uint2 *)((char *)workspace + chunk_bytes(rows, n));
-    hipStream_t st = (hipStream_t)stream;
-    const dim3 grid(a.C, rows);
-    if (vpt == 4) {
-        hipLaunchKernelGGL(topk_hist_kernel<4>, grid, dim3(TB), 0, st, a);
-        hipLaunchKernelGGL(topk_boundary_kernel<4>, grid, dim3(TB), 0, st, a);
-        hipLaunchKernelGGL(topk_emit_kernel<4>, grid, dim3(TB), 0, st, a);
-    } else {
-        hipLaunchKernelGGL(topk_hist_kernel<16>, grid, dim3(TB), 0, st, a);
-        hipLaunchKernelGGL(topk_boundary_kernel<16>, grid, dim3(TB), 0, st, a);
-        hipLaunchKernelGGL(topk_emit_kernel<16>, grid, dim3(TB), 0, st, a);
+    return topk_launch<false>(a, rows, vpt, (hipStream_t)stream, "ma_topk_select");
+}
+
+extern "C" int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const float *score,
+                              int64_t score_stride, int rows, int n, int capacity, int window, int64_t sink_tokens,
+                              const int64_t *pin_lo_rows, int64_t pin_lo, int64_t pin_hi, int has_pin, int64_t *keep,
+                              int64_t keep_stride, int32_t *status, void *state, int64_t state_bytes,
+                              void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!pos || !score || !keep || rows < 0 || n < 0 || capacity < 0 || capacity > n || window < 0 ||
+        keep_stride < capacity || pos_stride < n || score_stride < n || rows > 65535) {
+        ma_set_error("ma_keep_select: bad arguments (rows=%d n=%d capacity=%d window=%d)", rows, n, capacity,
+                     window);
+        return MA_EINVAL;
     }
-    return ma_check_launch("ma_topk_select");
+    if (rows == 0 || capacity == 0) return MA_OK;
+    const int w = window < capacity ? window : capacity;
+    TopkArgs a;
+    int vpt = 0;
+    const int rc = topk_prepare(a, vpt, "ma_keep_select", score, score_stride, rows, n, capacity - w, keep,
+                                keep_stride, state, state_bytes, workspace, workspace_bytes);
+    if (rc) return rc;
+    a.pos = pos;
+    a.pos_i64 = pos_is_i64 != 0;
+    a.pos_stride = pos_stride;
+    a.m = n - w;
+    a.w = w;
+    a.has_pin = has_pin != 0;
+    a.sink = sink_tokens;
+    a.pin_lo = pin_lo;
+    a.pin_hi = pin_hi;
+    a.pin_lo_rows = pin_lo_rows;
+    a.status = status;
+    return topk_launch<true>(a, rows, vpt, (hipStream_t)stream, "ma_keep_select");
 }

@@ -17,6 +17,7 @@ import os
 import torch
 
 from .. import _native as N
+from .select import _state as select_state
 
 
 def keep_select(pos: torch.Tensor, score: torch.Tensor, capacity: int, window: int, *, sink_tokens: int = 0,
@@ -66,10 +67,16 @@ def keep_select(pos: torch.Tensor, score: torch.Tensor, capacity: int, window: i
         else:
             lo = int(lo)
     lib = N.load()
+    ws_bytes = int(lib.ma_topk_workspace_bytes(rows, n))
+    if ws_bytes <= 0:
+        raise N.KernelUnavailableError(f"ma_keep_select: n={n} exceeds the built maximum")
+    st = select_state(score.device, int(lib.ma_topk_state_bytes(rows)))
+    ws = torch.empty((ws_bytes,), device=score.device, dtype=torch.uint8)
     rc = lib.ma_keep_select(p2.data_ptr(), 1 if p2.dtype == torch.int64 else 0, p2.stride(0) if rows > 1 else n,
                             s2.data_ptr(), s2.stride(0) if rows > 1 else n, rows, n, capacity, int(window),
                             int(sink_tokens), N.ptr(lo_rows), lo, hi, has_pin, out.data_ptr(), capacity,
-                            status.data_ptr(), N.stream_of(score))
+                            status.data_ptr(), st.data_ptr(), st.numel(), ws.data_ptr(), ws.numel(),
+                            N.stream_of(score))
     N.check(rc, "ma_keep_select")
     if check and bool(status.any()):
         raise ValueError("keep_select: live positions must increase strictly along each lane")

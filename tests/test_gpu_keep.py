@@ -29,7 +29,8 @@ def _positions(rows, n, g, gap_p=0.3):
 
 @pytest.mark.parametrize("n,cap,window,sinks,pin", [
     (1, 1, 0, 0, None), (300, 40, 16, 4, None), (300, 300, 8, 0, None), (1000, 256, 128, 4, (50, 90)),
-    (5000, 700, 0, 0, None), (4096, 1024, 128, 4, None), (65536, 8192, 128, 4, (1000, 1200)), (40000, 39000, 500, 0, None)])
+    (5000, 700, 0, 0, None), (4096, 1024, 128, 4, None), (65536, 8192, 128, 4, (1000, 1200)), (40000, 39000, 500, 0, None),
+    (131072, 4096, 128, 4, (5000, 6000)), (1_050_003, 30000, 64, 4, None)])
 def test_keep_select_bit_exact(gpu, n, cap, window, sinks, pin):
     g = torch.Generator().manual_seed(n + cap)
     rows = 6
@@ -61,6 +62,24 @@ def test_keep_select_per_row_pin_and_unsorted_rejected(gpu):
     bad[2, 100], bad[2, 101] = bad[2, 101], bad[2, 100]
     with pytest.raises(ValueError):
         keep_select(bad.to(gpu), score.to(gpu), 100, 10)
+    # a violation exactly across a 1024-entry chunk boundary, and one inside the window
+    pos2 = _positions(3, 5000, g)
+    s2 = torch.rand((3, 5000), generator=g)
+    pos2[1, 1024] = pos2[1, 1023]
+    pos2[2, 4990] = pos2[2, 4989] - 1
+    from maskahead_amd import _native as N
+    from maskahead_amd.kernels.select import _state
+    lib = N.load()
+    st = torch.zeros((3,), dtype=torch.int32, device=gpu)
+    out = torch.empty((3, 300), dtype=torch.int64, device=gpu)
+    ws = torch.empty((int(lib.ma_topk_workspace_bytes(3, 5000)),), dtype=torch.uint8, device=gpu)
+    state = _state(torch.device(gpu), int(lib.ma_topk_state_bytes(3)))
+    pg, sg = pos2.to(gpu), s2.to(gpu)
+    rc = lib.ma_keep_select(pg.data_ptr(), 1, 5000, sg.data_ptr(), 5000, 3, 5000, 300, 20, 0, None, 0, 0, 0,
+                            out.data_ptr(), 300, st.data_ptr(), state.data_ptr(), state.numel(), ws.data_ptr(),
+                            ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert st.cpu().tolist() == [0, 1, 1]
 
 
 def _bf16(bits):
