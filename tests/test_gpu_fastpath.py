@@ -2,8 +2,8 @@
 (bf16 and packed int4 with the bf16 residual, cache.py:385-566), views (608-657),
 compaction (342-367), and FastLayerPath's step 0 (session.py:1403-1454), sub-step
 attention over the compact buffer (1286-1336) and block-causal probe attention with
-prefix mass (1378-1392), each against the CPU oracle on the same inputs.  The last test
-runs BASELINE config 3's keep/evict step at full size."""
+prefix mass (1378-1392), each against the CPU oracle on the same inputs.  Then BASELINE
+config 3's keep/evict step at full size, and config 4's ragged batch at a reduced size."""
 
 import pytest
 import torch
@@ -196,3 +196,49 @@ def test_config3_keep_step(gpu):
     _fill(cache, [(kc[:, :, :32], vc[:, :, :32])], gpu)
     assert cache.length == sh.keep_k + 32
     assert torch.equal(cache.layer_view(0).k_fp[:, :, sh.keep_k:].cpu(), kc[:, :, :32])
+
+
+def test_config4_ragged_batch_step0_and_keep(gpu):
+    """BASELINE config 4's structure at a CPU-checkable size: a batch of sequences with
+    different prefix lengths in one packed int4 cache (the slots past each sequence's
+    length dead in the layer's slot mask), two layers of the config-1 head shape, step 0
+    of every layer (attention, value-aware read set of 512 over live slots, gather), then
+    each sequence's keep set (budget 1024, window 64, 4 sinks) over its live entries."""
+    b, hq, hkv, d, t, k_read, keep_k = 3, 28, 4, 128, 32, 512, 1024
+    lens = [1536, 3200, 4064]
+    n = max(lens)
+    q, k, v, kc, vc = layer_inputs(b=b, hq=hq, hkv=hkv, d=d, n=n, t=t, seed=44)
+    cache = PackedKVCache(num_layers=2, batch_size=b, num_kv_heads=hkv, head_dim=d, max_tokens=n + 64,
+                          quant=QuantizationConfig(), device=gpu)
+    _fill(cache, [(k, v)], gpu)
+    mask = torch.zeros((b, hkv, n), dtype=torch.uint8)
+    for i, ln in enumerate(lens):
+        mask[i, :, :ln] = 1
+    fp = FastLayerPath(cache=cache, block_size=t, query_indices=list(range(t)),
+                       slot_masks={l: mask.to(gpu) for l in range(2)})
+    qb, kcb, vcb = q.to(torch.bfloat16), kc.to(torch.bfloat16), vc.to(torch.bfloat16)
+    for layer in range(2):
+        kd, vd, _ = _oracle_packed_layer(k + layer, v)
+        out = fp.step0(layer, qb.to(gpu), kcb.to(gpu), vcb.to(gpu), select=True, topk=k_read, want_mass=True)
+        wout, wmp, wlp, wop = OA.splitk_attention(qb, kd, vd, kcb, vcb, mask=mask)
+        assert_attention_close(out, wout)
+        wmass, wscore = OA.prefix_scores(qb, kd, vd.float(), wmp, wlp, wop, list(range(t)), mask=mask,
+                                         value_aware=True)
+        assert rel_err(fp.last_mass[layer].cpu() + (1 - mask), wmass + (1 - mask)) < 2e-3
+        st = fp.states[layer]
+        idx = st.indices.cpu()
+        ok, nmis, worst = OS.boundary_mismatch_ok(idx, OS.topk_ascending(wscore, k_read, mask), wscore, k_read,
+                                                  rel=2e-3, mask=mask)
+        assert ok, (layer, nmis, worst)
+        assert bool(torch.all(mask.gather(2, idx) == 1))          # only live slots are read
+        gi = idx.unsqueeze(-1).expand(-1, -1, -1, d)
+        assert torch.equal(st.key[:, :, :k_read].cpu(), kd.gather(2, gi))
+        assert torch.equal(st.value[:, :, :k_read].cpu(), vd.gather(2, gi))
+        # eviction: each sequence's keep set over its live entries, bit-exact vs the oracle
+        mass = fp.last_mass[layer]
+        for i, ln in enumerate(lens):
+            pos = torch.arange(ln, dtype=torch.int64).expand(1, hkv, ln)
+            sc = mass[i:i + 1, :, :ln]
+            keep = keep_select(pos.to(gpu), sc, keep_k, 64, sink_tokens=4)
+            wkeep = OS.keep_select(pos.reshape(-1, ln), sc.cpu().reshape(-1, ln), keep_k, 64, 4)
+            assert torch.equal(keep.cpu().reshape(-1, keep_k), wkeep), (layer, i)
