@@ -63,15 +63,26 @@ struct FwdSmem {
     uint64_t kmask[2];         // usable tokens of the K tile in each buffer
     float fin[MAXS][3][32];    // final m_ref, m_true, l of every row
 };
+// after the last PV, the P^T buffers hold each O wave's 32 x D f16 tile of O (write_partial)
+static_assert(sizeof(FwdSmem<128>::p) >= MAXS * 32 * 128 * 2, "P buffers too small for the O tiles");
 
-// write a row's partial: max in natural-log units, the sum of exp relative to it, and the
-// normalized output O = acc / l as f16 on a per-row scale (the row's max |O|), so the
-// partial is half the size of an f32 one and cannot overflow.
+// write a row tile's partials: per row the max in natural-log units, the sum of exp
+// relative to it, and the normalized output O = acc / l as f16 on a per-row scale (the
+// row's max |O|), so the partial is half the size of an f32 one and cannot overflow.  The
+// wave's 32 x D tile of O goes through its own LDS region (16-byte granules, XOR-swizzled
+// by row) so that every global store instruction writes whole rows, contiguously: the
+// tile's rows are adjacent in wo.  Called by the whole wave; rows >= R are not written.
 template <int D>
 __device__ __forceinline__ void write_partial(const FwdArgs &a, const f32x16_t *acc, float m_ref, float m_true,
-                                              float l, int bh, int slot, int row, int hf) {
+                                              float l, int bh, int slot, int rtile, int c32, int hf, int lane,
+                                              uint4 *lds) {
     constexpr int NDT = D / 32;
-    const int64_t prow = ((int64_t)bh * (a.nsplit + 1) + slot) * a.R + row;
+    constexpr int NG = D / 8;       // 16-byte granules per row
+    constexpr int RPI = 64 / NG;    // rows per store instruction
+    typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
+    const int row0 = rtile * 32;
+    const int64_t prow0 = ((int64_t)bh * (a.nsplit + 1) + slot) * a.R + row0;
+    const int nrows = min(32, a.R - row0);
     float mx = 0.f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -79,23 +90,34 @@ __device__ __forceinline__ void write_partial(const FwdArgs &a, const f32x16_t *
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(acc[dt][i]));
     mx = ma_max_xor32(mx);                       // the row's other half lives in lane ^ 32
     const float inv = mx > 0.f ? 1.0f / mx : 0.f;
-    if (hf == 0) {
+    if (hf == 0 && c32 < nrows) {
         float f = 0.f;
         if (m_true != -INFINITY) f = __builtin_amdgcn_exp2f((m_ref - m_true) * a.sl2);
-        a.wm[prow] = m_true * a.scale;
-        a.wl[prow] = l * f;
-        a.wsc[prow] = l > 0.f ? mx / l : 0.f;    // O = acc / l = wo * wsc
+        a.wm[prow0 + c32] = m_true * a.scale;
+        a.wl[prow0 + c32] = l * f;
+        a.wsc[prow0 + c32] = l > 0.f ? mx / l : 0.f;    // O = acc / l = wo * wsc
     }
-    _Float16 *dst = a.wo + prow * D;
+    // lane (c32, hf) holds columns dt * 32 + q4 * 8 + hf * 4 + (0..3) of row c32
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-            typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
             const f16x4_t v = {(_Float16)(acc[dt][q4 * 4 + 0] * inv), (_Float16)(acc[dt][q4 * 4 + 1] * inv),
                                (_Float16)(acc[dt][q4 * 4 + 2] * inv), (_Float16)(acc[dt][q4 * 4 + 3] * inv)};
-            *(f16x4_t *)&dst[dt * 32 + q4 * 8 + hf * 4] = v;
+            const int g = (dt * 4 + q4) ^ (c32 % NG);
+            *(f16x4_t *)((char *)&lds[c32 * NG + g] + hf * 8) = v;
         }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint4 *dst = (uint4 *)(a.wo + prow0 * D);
+    const int g = lane % NG;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+        const int r = i * RPI + lane / NG;
+        const uint4 v = lds[r * NG + (g ^ (r % NG))];
+        if (r < nrows) dst[r * NG + g] = v;
+    }
 }
 
 // S wave: S^T = K Q^T for one 64-token tile (A = K rows from LDS, B = Q^T in registers).
@@ -329,8 +351,9 @@ __device__ __forceinline__ void cur_segment(const FwdArgs &a, const Work &wk, Fw
             __syncthreads();  // PV done
         }
         __syncthreads();  // final statistics
-        if (is_o && row_ok)
-            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, a.nsplit, row, hf);
+        if (is_o)
+            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, a.nsplit,
+                             wk.rg * MAXS + rw, c32, hf, lane, &S.p[0][0][0][0] + rw * (4 * D));
     }
 }
 
@@ -589,8 +612,9 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             __syncthreads();
         }
         __syncthreads();  // final statistics of the S waves
-        if (is_o && row_ok)
-            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, slot, row, hf);
+        if (is_o)
+            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, slot, rtile, c32,
+                             hf, lane, &S.p[0][0][0][0] + rw * (4 * D));
     }
 }
 
