@@ -64,3 +64,47 @@ def assert_attention_close(got: torch.Tensor, want: torch.Tensor, atol=2e-2, rto
 
 
 __all__ = ["layer_inputs", "packed_cpu", "gpu_prefix", "dequant_cpu", "rel_err", "assert_attention_close"]
+
+
+REBUILD_GOLD = "rebuild_vectors.npz"
+REBUILD_CASES = ("lazy", "lazy2", "full", "stage", "tail")
+
+
+def rebuild_case(tag: str) -> dict:
+    """One eviction case written by the reference (tests/golden/make_rebuild_golden.py):
+    storage before / after as CPU tensors, lengths, the state's pos / phys, the keep set,
+    the settings and the slots after."""
+    from pathlib import Path
+
+    import numpy as np
+
+    z = np.load(Path(__file__).resolve().parent / "golden" / REBUILD_GOLD)
+
+    def t16(a, dt):
+        return torch.from_numpy(a.view(np.int16)).view(dt)
+
+    def store(io):
+        f = lambda k: z[f"{tag}_{io}_{k}"]  # noqa: E731
+        return {"kq": torch.from_numpy(f("kq")), "ks": t16(f("ks"), torch.float16),
+                "kz": t16(f("kz"), torch.float16), "vq": torch.from_numpy(f("vq")),
+                "vs": t16(f("vs"), torch.float16), "vz": t16(f("vz"), torch.float16),
+                "kr": t16(f("kr"), torch.bfloat16), "vr": t16(f("vr"), torch.bfloat16)}
+
+    live, next_pos, stage, window, mode, rb = (int(x) for x in z[f"{tag}_cfg"])
+    return {"in": store("in"), "out": store("out"),
+            "in_lens": tuple(int(x) for x in z[f"{tag}_in_lens"]),
+            "out_lens": tuple(int(x) for x in z[f"{tag}_out_lens"]),
+            "pos": torch.from_numpy(z[f"{tag}_pos"]), "phys": torch.from_numpy(z[f"{tag}_phys"]),
+            "keep": torch.from_numpy(z[f"{tag}_keep"]), "out_phys": torch.from_numpy(z[f"{tag}_out_phys"]),
+            "next_position": next_pos, "stage_mode": bool(stage), "recent_window": window,
+            "mode": ("lazy", "full")[mode], "repack_below": rb / 1000.0}
+
+
+def same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Equal shapes and identical bits (16-bit floats compared as integers)."""
+    a, b = a.detach().cpu().contiguous(), b.detach().cpu().contiguous()
+    if a.shape != b.shape or a.dtype != b.dtype:
+        return False
+    if a.element_size() == 2 and a.is_floating_point():
+        a, b = a.view(torch.int16), b.view(torch.int16)
+    return torch.equal(a, b)
