@@ -208,6 +208,43 @@ int ma_quantize_keys(ma_tensor4 src, int B, int H, int T, int D, int group, void
 int ma_quantize_values(ma_tensor4 src, int B, int H, int T, int D, int group, void *vq,
                        const int64_t svq[4], void *vs, void *vz, const int64_t svs[3], void *stream);
 
+/* f1. packed eviction rebuild, plan half: the lists of the session's lazy / full
+ * compaction (runtime/session.py:288-345, BitSieveSession._evict_to) for `lanes`
+ * (layer, batch, KV head) lanes of `live` live entries each.  phys int32 (old slot of
+ * each live entry, < 2^24) and pos (int32, or int64 if pos_is_i64) have lane strides
+ * phys_stride / pos_stride.  A key group of the old quantized part [0, quantized_length)
+ * is kept when it holds >= need live entries and is not one of its last tail_groups
+ * groups (need > 32: none, the "full" mode); the window newest entries outside the
+ * quantized part stay bf16; every other entry is re-encoded.  Outputs per lane, padded
+ * with -1: groups_before [max(1, quantized_length/32)] kept group ids ascending,
+ * encode [live] and stage [live] old slots in (position, slot) order; counts [lanes][3]
+ * int32 = (kept groups, encoded, staged), all -1 for a lane out of (position, slot)
+ * order with more than 16384 live entries (not built).  The caller pads the lists to
+ * the largest count of any lane, as the reference does. */
+int ma_rebuild_plan(const int32_t *phys, int64_t phys_stride, const void *pos, int pos_is_i64,
+                    int64_t pos_stride, int lanes, int live, int quantized_length, int need, int tail_groups,
+                    int window, int64_t *groups_before, int64_t gb_stride, int64_t *encode, int64_t enc_stride,
+                    int64_t *stage, int64_t stage_stride, int32_t *counts, void *stream);
+
+/* f1. packed eviction rebuild, data half: PackedKVCache.rebuild (cache.py:236-335) of the
+ * B x H lanes of old_store into new_store (both as ma_prefix: nq = quantized length, kf/vf
+ * = the bf16 residual of nf entries; new_store's pointers are written).  The new lane
+ * is [groups_before | encode quantized into ceil(m/32) groups | groups_after] + stage as
+ * the new residual: old key groups copied byte for byte (a -1 entry copies group 0),
+ * old slots dequantized to bf16 and quantized again in bf16 arithmetic (-1 and the
+ * padding of the last group: zeros), old slots kept as bf16 rows (-1: zeros).  Lists are
+ * int64 [lanes][width] with lane strides.  remap int64 [lanes][old length] (lane stride
+ * remap_stride) = new slot of every old slot, -1 if dropped (a later list wins a slot
+ * named twice: groups, then encode, then stage).  phys (optional, int32, lane stride
+ * phys_stride, live entries) is rewritten through remap (EvictionState slots,
+ * session.py:352-355).  status int32 [lanes]: bit 0 = a list entry outside the old
+ * storage (ignored), bit 1 = a live entry with no new slot. */
+int ma_rebuild_packed(const ma_prefix *old_store, int B, int H, int D, const ma_prefix *new_store,
+                      const int64_t *groups_before, int64_t gb_stride, int g1, const int64_t *encode,
+                      int64_t enc_stride, int m, const int64_t *groups_after, int64_t ga_stride, int g3,
+                      const int64_t *stage, int64_t stage_stride, int st, int64_t *remap, int64_t remap_stride,
+                      int32_t *phys, int64_t phys_stride, int live, int32_t *status, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

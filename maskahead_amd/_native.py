@@ -80,6 +80,9 @@ SIGNATURES = {
     "ma_gather_kv": (_I, [_PREF, _I, _I, _I, _P, _I64P, _I, _T4, _T4, _P]),
     "ma_quantize_keys": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),
     "ma_quantize_values": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),
+    "ma_rebuild_plan": (_I, [_P, _I64, _P, _I, _I64, _I, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P]),
+    "ma_rebuild_packed": (_I, [_PREF, _I, _I, _I, _PREF, _P, _I64, _I, _P, _I64, _I, _P, _I64, _I, _P, _I64, _I,
+                               _P, _I64, _P, _I64, _I, _P, _P]),
 }
 
 _lib = None
@@ -114,6 +117,11 @@ def check(rc: int, what: str) -> None:
     if rc == MA_EUNSUPPORTED:
         raise KernelUnavailableError(msg)
     raise RuntimeError(msg)
+
+
+def call(name: str, *args) -> None:
+    """Call entry point `name` of the library; a negative status raises (check)."""
+    check(getattr(load(), name)(*args), name)
 
 
 def require_gpu(t: torch.Tensor, name: str = "tensor") -> None:

@@ -13,7 +13,7 @@ re-appends.
 Built for 4-bit (key groups of 32 tokens per channel, value groups of 32 channels per
 token, f16 scale/zero) and 16-bit layouts; other valid quantization settings raise
 KernelUnavailableError.  The packed lazy rebuild (``stage`` / ``rebuild``,
-cache.py:236-335) is not part of this build.
+cache.py:236-335) runs in one launch of ma_rebuild_packed over every layer.
 """
 
 from __future__ import annotations
@@ -390,6 +390,73 @@ class PackedKVCache:
         if self.capacity > 2 * c + 2048:
             self._resize(c + 1024)
         self._note_peak()
+
+    # -- packed eviction rebuild (cache.py:236-335) ----------------------------------------
+    def _fold(self, t: torch.Tensor | None) -> torch.Tensor | None:
+        """[L, B, H, ...] storage -> [L*B, H, ...] view: every layer in one launch."""
+        return None if t is None else t.flatten(0, 1)
+
+    def rebuild(self, groups_before: torch.Tensor, encode: torch.Tensor, groups_after: torch.Tensor,
+                stage: torch.Tensor) -> torch.Tensor:
+        """New physical layout [groups_before | encoded | groups_after] + bf16 staging
+        (cache.py:236-335).  Index tensors [L, B, H, n] int64, padded with -1:
+        groups_before / groups_after old key groups copied bit-exactly (a -1 entry holds a
+        copy of group 0 and must be masked by the caller), encode old slots quantized into
+        fresh groups, stage old slots kept in bf16 (the new residual; -1: zeros).  Returns
+        remap [L, B, H, old_length]: the new slot of every old slot, -1 if dropped."""
+        return self._rebuild(groups_before, encode, groups_after, stage)
+
+    def _rebuild(self, groups_before, encode, groups_after, stage, phys: torch.Tensor | None = None,
+                 live: int = 0) -> torch.Tensor:
+        """rebuild(); phys (the eviction state's int32 [L, B, H, capacity] slots) is
+        rewritten through the remap in the same launch (session.py:352-355)."""
+        from .kernels.rebuild import rebuild_packed
+        from .kernels.splitk import Prefix
+
+        if self._append_plan is not None:
+            raise RuntimeError("rebuild during an append")
+        if self.k_q is None or self.v_q is None:
+            raise ValueError("rebuild needs a packed (k_bits, v_bits < 16) cache")
+        gk = self.quant.key_token_group
+        L, B, H, D = self.num_layers, self.batch_size, self.num_kv_heads, self.head_dim
+        lead = (L, B, H)
+        for name, t in (("groups_before", groups_before), ("encode", encode), ("groups_after", groups_after),
+                        ("stage", stage)):
+            if t.dim() != 4 or tuple(t.shape[:3]) != lead:
+                raise ValueError(f"{name} must be [L, B, H, n], got {tuple(t.shape)}")
+        dev = self.device
+        old_len, old_q, old_r = self.length, self.quantized_length, self.residual_length
+        g1, m, g3, st = groups_before.shape[-1], encode.shape[-1], groups_after.shape[-1], stage.shape[-1]
+        g2 = -(-m // gk)
+        ql = (g1 + g2 + g3) * gk
+        new_len = ql + st
+        cap = new_len + 1024
+        ng_cap = -(-cap // gk)
+        kq = torch.empty((L, B, H, ng_cap, D, self.k_q.shape[-1]), device=dev, dtype=self.k_q.dtype)
+        ks = torch.empty((L, B, H, ng_cap, D), device=dev, dtype=self.k_scale.dtype)
+        kz = torch.empty_like(ks)
+        vq = torch.empty((L, B, H, cap, *self.v_q.shape[4:]), device=dev, dtype=self.v_q.dtype)
+        vs = torch.empty((L, B, H, cap, self.v_scale.shape[-1]), device=dev, dtype=self.v_scale.dtype)
+        vz = torch.empty_like(vs)
+        rcap = max(st + 256, 64)
+        kr = torch.empty((L, B, H, rcap, D), device=dev, dtype=self.k_residual.dtype)
+        vr = torch.empty_like(kr)
+        remap = torch.empty((L, B, H, old_len), device=dev, dtype=torch.int64)
+        f = self._fold
+        old = Prefix(kq=f(self.k_q), ks=f(self.k_scale), kz=f(self.k_zero), vq=f(self.v_q), vs=f(self.v_scale),
+                     vz=f(self.v_zero), kf=f(self.k_residual), vf=f(self.v_residual), nq=old_q, nf=old_r,
+                     kb=4, vb=4)
+        new = Prefix(kq=f(kq), ks=f(ks), kz=f(kz), vq=f(vq), vs=f(vs), vz=f(vz), kf=f(kr), vf=f(vr), nq=ql, nf=st,
+                     kb=4, vb=4)
+        rebuild_packed(old, new, B=L * B, H=H, D=D, groups_before=groups_before, encode=encode,
+                       groups_after=groups_after, stage=stage, remap=remap, phys=phys, live=live)
+        self.k_q, self.k_scale, self.k_zero, self.v_q, self.v_scale, self.v_zero = kq, ks, kz, vq, vs, vz
+        self.k_residual, self.v_residual = kr, vr
+        self.capacity, self.residual_capacity = cap, rcap
+        self.length, self.quantized_length, self.residual_length = new_len, ql, st
+        self.dropped += old_len - new_len
+        self._note_peak()
+        return remap
 
     # -- memory accounting (cache.py:753-811) ----------------------------------------------
     def allocated_nbytes(self) -> int:

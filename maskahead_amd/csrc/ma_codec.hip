@@ -2,6 +2,7 @@
 // 4-bit quantizers of the append path.  All integer/byte work, bit-exact against the
 // reference's torch codec (reference.py:35-268).
 #include "ma_common.h"
+#include "ma_quant.h"
 
 namespace {
 
@@ -189,31 +190,6 @@ __global__ void __launch_bounds__(256) gather_kernel(PrefixArgs a, int H, int D,
 }
 
 // ---------------------------------------------------------------- quantizers
-// Arithmetic "in the source dtype": every op computed in f32 and rounded to the source
-// type, which is how torch's CPU kernels evaluate bf16/f16 tensors (reference.py:78-81).
-__device__ __forceinline__ float rnd(float x, int dtype) {
-    if (dtype == MA_BF16) return ma_round_bf16(x);
-    if (dtype == MA_F16) return ma_round_f16(x);
-    return x;
-}
-
-struct QuantGroup {
-    float lo, step;
-};
-
-__device__ __forceinline__ QuantGroup quant_params(float lo, float hi, int dtype) {
-    float step = rnd(rnd(hi - lo, dtype) / 15.0f, dtype);
-    step = rnd(fmaxf(step, 1e-8f), dtype);
-    return {lo, step};
-}
-
-__device__ __forceinline__ uint32_t quant_code(float x, QuantGroup q, int dtype) {
-    float r = rnd(rnd(x - q.lo, dtype) / q.step, dtype);
-    float c = __builtin_rintf(r);  // half to even
-    c = fminf(fmaxf(c, 0.0f), 15.0f);
-    return (uint32_t)c;
-}
-
 // keys: grid (T/KG, B*H), D threads; thread = one channel of one token group.
 __global__ void quantize_keys_kernel(ma_tensor4 src, int H, int D, uint8_t *kq, int64_t q0, int64_t q1, int64_t q2,
                                      int64_t q3, _Float16 *ks, _Float16 *kz, int64_t s0, int64_t s1, int64_t s2) {

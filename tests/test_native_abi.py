@@ -66,3 +66,24 @@ def test_unsupported_prefix_is_reported(lib):
     rc = lib.ma_splitk_attention(N.MaTensor4(), 1, 28, 32, 96, p, 4, N.MaTensor4(), N.MaTensor4(), 0, 0, 0, 0,
                                  1.0, N.MaTensor4(), None, None, None, 0, None, 0, None)
     assert rc == N.MA_EUNSUPPORTED          # head_dim 96 is not built
+
+
+def test_rebuild_arguments_are_checked_on_the_host(lib):
+    """ma_rebuild_plan / ma_rebuild_packed reject bad sizes before any launch."""
+    # window larger than the live count
+    rc = lib.ma_rebuild_plan(1, 8, 1, 0, 8, 1, 4, 64, 16, 0, 5, 1, 2, 1, 8, 1, 8, 1, None)
+    assert rc == N.MA_EINVAL and b"bad sizes" in lib.ma_last_error()
+    # quantized length not a multiple of the key group
+    rc = lib.ma_rebuild_plan(1, 8, 1, 0, 8, 1, 4, 40, 16, 0, 0, 1, 2, 1, 8, 1, 8, 1, None)
+    assert rc == N.MA_EINVAL
+    # more key groups than the plan counts in LDS
+    rc = lib.ma_rebuild_plan(1, 8, 1, 0, 8, 1, 4, 32 * 40000, 16, 0, 0, 1, 40000, 1, 8, 1, 8, 1, None)
+    assert rc == N.MA_EUNSUPPORTED
+    # no old storage; then new storage whose length disagrees with the lists
+    rc = lib.ma_rebuild_packed(None, 1, 1, 64, None, None, 0, 0, None, 0, 0, None, 0, 0, None, 0, 0, None, 0,
+                               None, 0, 0, None, None)
+    assert rc == N.MA_EINVAL
+    old, new = N.MaPrefix(), N.MaPrefix()
+    rc = lib.ma_rebuild_packed(old, 1, 1, 64, new, None, 0, 1, None, 0, 0, None, 0, 0, None, 0, 0, None, 0,
+                               None, 0, 0, None, None)   # one kept group, but new storage of 0 entries
+    assert rc == N.MA_EINVAL and b"expected" in lib.ma_last_error()
