@@ -233,7 +233,8 @@ int ma_rebuild_plan(const int32_t *phys, int64_t phys_stride, const void *pos, i
  * the new residual: old key groups copied byte for byte (a -1 entry copies group 0),
  * old slots dequantized to bf16 and quantized again in bf16 arithmetic (-1 and the
  * padding of the last group: zeros), old slots kept as bf16 rows (-1: zeros).  Lists are
- * int64 [lanes][width] with lane strides.  remap int64 [lanes][old length] (lane stride
+ * int64 [lanes][width] with lane strides (0: one list for every lane).  remap int64
+ * [lanes][old length] (lane stride
  * remap_stride) = new slot of every old slot, -1 if dropped (a later list wins a slot
  * named twice: groups, then encode, then stage).  phys (optional, int32, lane stride
  * phys_stride, live entries) is rewritten through remap (EvictionState slots,

@@ -21,6 +21,8 @@
 //   sources at index >= C, which no launch writes, directly from the cache.
 //
 // append (cache.py:385-566, bf16 layout): dst[b, h, at + t, :] = src[b, h, t, :].
+#include <algorithm>
+
 #include "ma_common.h"
 
 namespace {
@@ -195,6 +197,7 @@ constexpr int MAX_PLANES = 8;
 struct CompactArgs {
     Plane pl[MAX_PLANES];
     int nplanes, H, C, n;
+    int lpe;              // threads per entry: the widest plane's copy units, a power of two <= 16
     const int64_t *keep;
     int64_t skb, skh;     // keep strides (elements), entries contiguous
     char *scratch;        // [rows][C][total_row_bytes]
@@ -234,13 +237,13 @@ __device__ __forceinline__ void copy_bytes(char *d, const char *s, int bytes, in
     }
 }
 
-// grid (ceil(C / 16), rows), 256 threads: 16 entries x 16 lanes.
+// grid (ceil(C / (256 / lpe)), rows), 256 threads: 256 / lpe entries x lpe lanes.
 // PHASE 0: sources inside [0, C) that move -> scratch.  PHASE 1: every destination.
 template <int PHASE>
 __global__ void __launch_bounds__(256) compact_kernel(CompactArgs a) {
     const int row = blockIdx.y, b = row / a.H, h = row % a.H;
-    const int i = blockIdx.x * 16 + threadIdx.x / 16;
-    const int lane = threadIdx.x % 16;
+    const int i = blockIdx.x * (256 / a.lpe) + threadIdx.x / a.lpe;
+    const int lane = threadIdx.x % a.lpe;
     if (i >= a.C) return;
     const int64_t src = a.keep[(int64_t)b * a.skb + (int64_t)h * a.skh + i];
     const bool valid = src >= 0 && src < a.n;
@@ -251,10 +254,11 @@ __global__ void __launch_bounds__(256) compact_kernel(CompactArgs a) {
         const Plane &P = a.pl[p];
         char *lane_base = P.base + b * P.sb + h * P.sh;
         if (PHASE == 0) {
-            if (inside) copy_bytes(srow + a.plane_off[p], lane_base + src * P.sn, P.row_bytes, P.unit, lane, 16, false);
+            if (inside) copy_bytes(srow + a.plane_off[p], lane_base + src * P.sn, P.row_bytes, P.unit, lane, a.lpe,
+                                   false);
         } else {
             const char *from = inside ? srow + a.plane_off[p] : lane_base + (valid ? src : 0) * P.sn;
-            copy_bytes(lane_base + (int64_t)i * P.sn, from, P.row_bytes, P.unit, lane, 16, !valid);
+            copy_bytes(lane_base + (int64_t)i * P.sn, from, P.row_bytes, P.unit, lane, a.lpe, !valid);
         }
     }
 }
@@ -368,6 +372,11 @@ extern "C" int ma_compact_tokens(void *const *bases, const int64_t *strides, con
         ca.plane_off[p] = (int32_t)tot;
         tot += ((int64_t)P.row_bytes + 15) & ~(int64_t)15;
     }
+    int units = 1;
+    for (int p = 0; p < nplanes; ++p)
+        units = std::max(units, (int)((ca.pl[p].row_bytes + ca.pl[p].unit - 1) / ca.pl[p].unit));
+    ca.lpe = 1;
+    while (ca.lpe < 16 && ca.lpe < units) ca.lpe <<= 1;
     const int64_t need = (int64_t)B * H * capacity * tot + 256;
     if (!workspace || workspace_bytes < need) {
         ma_set_error("%s: workspace %lld bytes < %lld needed", who, (long long)workspace_bytes, (long long)need);
@@ -384,7 +393,8 @@ extern "C" int ma_compact_tokens(void *const *bases, const int64_t *strides, con
     ca.scratch = (char *)(((uintptr_t)workspace + 15) & ~(uintptr_t)15);
     ca.total_row_bytes = tot;
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((capacity + 15) / 16, B * H);
+    const int per_block = 256 / ca.lpe;
+    const dim3 grid((capacity + per_block - 1) / per_block, B * H);
     hipLaunchKernelGGL(compact_kernel<0>, grid, dim3(256), 0, st, ca);
     hipLaunchKernelGGL(compact_kernel<1>, grid, dim3(256), 0, st, ca);
     return ma_check_launch(who);

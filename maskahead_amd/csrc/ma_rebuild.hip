@@ -15,10 +15,12 @@
 //                   live entry classified in (position, slot) order -- the order the lanes
 //                   already hold after a keep-set selection, so the sort is skipped; lanes
 //                   out of that order are sorted in LDS (bitonic, up to 16384 entries).
-// ma_rebuild_packed one launch, four kinds of 256-thread workgroups: per lane the slot
-//                   remap (and the eviction state's slots rewritten through it), per new
-//                   group a byte copy or a requantization, per 32 staged entries a bf16
-//                   gather.  Old and new storage never alias.
+// ma_rebuild_packed two launches.  The first: 256-thread workgroups that fill the slot
+//                   remap with -1, copy a kept group byte for byte, requantize a new group
+//                   or gather 32 staged bf16 entries.  The second: one 1024-thread
+//                   workgroup per lane scatters the new slots into the remap in the
+//                   reference's list order and rewrites the eviction state's slots
+//                   through it.  Old and new storage never alias.
 #include "ma_common.h"
 #include "ma_quant.h"
 
@@ -307,48 +309,77 @@ __device__ __forceinline__ int64_t list_at(const int64_t *p, int64_t stride, int
     return i < n ? p[lane * stride + i] : -1;
 }
 
-// Per lane: remap[old slot] = new slot or -1, written in the reference's order (kept
-// groups, tail groups, encoded, staged: a later list wins a slot named twice), then the
-// eviction state's slots rewritten through it.  status bit 0: a list names a slot or
-// group outside the old storage; bit 1: a live entry's slot maps to no new slot.
-__device__ void remap_lane(const RbArgs &a, int lane) {
+// Per lane, after the fill of the data launch: remap[old slot] = new slot, written in the
+// reference's order (kept and tail groups, encoded, staged: a later list wins a slot
+// named twice), then the eviction state's slots rewritten through it.  Each thread loads
+// RM_BATCH list entries before it stores any, so a phase costs about one round trip.
+// status bit 0: a list names a slot or group outside the old storage; bit 1: a live
+// entry's slot maps to no new slot.
+constexpr int RM_THREADS = 1024;
+constexpr int RM_BATCH = 8;
+
+__global__ void __launch_bounds__(RM_THREADS) remap_kernel(RbArgs a) {
     __shared__ int flags;
-    const int tid = threadIdx.x;
+    const int lane = blockIdx.x, tid = threadIdx.x;
     int64_t *rm = a.remap + lane * a.sremap;
     if (tid == 0) flags = 0;
-    for (int i = tid; i < a.old_len; i += RB_THREADS) rm[i] = -1;
-    __syncthreads();
     int bad = 0;
     // kept and tail groups: every slot of a copied group, dead ones included
-    for (int u = tid; u < (a.g1 + a.g3) * KG; u += RB_THREADS) {
-        const int j = u / KG, t = u % KG;
-        const int64_t g = j < a.g1 ? list_at(a.gb, a.sgb, lane, a.g1, j) : list_at(a.ga, a.sga, lane, a.g3, j - a.g1);
-        const int dst = j < a.g1 ? j : a.g1 + a.g2 + (j - a.g1);
-        if (g < -1 || g >= a.old_ng) bad = 1;
-        else if (g >= 0) rm[g * KG + t] = (int64_t)dst * KG + t;
+    const int ngi = (a.g1 + a.g3) * KG;
+    for (int u0 = 0; u0 < ngi; u0 += RM_THREADS * RM_BATCH) {
+        int64_t g[RM_BATCH];
+#pragma unroll
+        for (int r = 0; r < RM_BATCH; ++r) {
+            const int u = u0 + r * RM_THREADS + tid, j = u / KG;
+            g[r] = u >= ngi ? -1 : j < a.g1 ? list_at(a.gb, a.sgb, lane, a.g1, j)
+                                            : list_at(a.ga, a.sga, lane, a.g3, j - a.g1);
+        }
+#pragma unroll
+        for (int r = 0; r < RM_BATCH; ++r) {
+            const int u = u0 + r * RM_THREADS + tid, j = u / KG, t = u % KG;
+            const int dst = j < a.g1 ? j : a.g1 + a.g2 + (j - a.g1);
+            if (g[r] < -1 || g[r] >= a.old_ng) bad = 1;
+            else if (u < ngi && g[r] >= 0) rm[g[r] * KG + t] = (int64_t)dst * KG + t;
+        }
     }
     __syncthreads();
-    for (int i = tid; i < a.m; i += RB_THREADS) {
-        const int64_t s = list_at(a.enc, a.senc, lane, a.m, i);
-        if (s < -1 || s >= a.old_len) bad = 1;
-        else if (s >= 0) rm[s] = (int64_t)a.g1 * KG + i;
-    }
+    auto scatter = [&](const int64_t *list, int64_t stride, int n, int64_t first) {
+        for (int i0 = 0; i0 < n; i0 += RM_THREADS * RM_BATCH) {
+            int64_t s[RM_BATCH];
+#pragma unroll
+            for (int r = 0; r < RM_BATCH; ++r) s[r] = list_at(list, stride, lane, n, i0 + r * RM_THREADS + tid);
+#pragma unroll
+            for (int r = 0; r < RM_BATCH; ++r) {
+                if (s[r] < -1 || s[r] >= a.old_len) bad = 1;
+                else if (s[r] >= 0) rm[s[r]] = first + i0 + r * RM_THREADS + tid;
+            }
+        }
+    };
+    scatter(a.enc, a.senc, a.m, (int64_t)a.g1 * KG);
     __syncthreads();
-    const int64_t nql = (int64_t)(a.g1 + a.g2 + a.g3) * KG;
-    for (int i = tid; i < a.st; i += RB_THREADS) {
-        const int64_t s = list_at(a.stg, a.sstg, lane, a.st, i);
-        if (s < -1 || s >= a.old_len) bad = 1;
-        else if (s >= 0) rm[s] = nql + i;
-    }
+    scatter(a.stg, a.sstg, a.st, (int64_t)(a.g1 + a.g2 + a.g3) * KG);
     __syncthreads();
     int lost = 0;
     if (a.phys) {
         int32_t *ph = a.phys + lane * a.sphys;
-        for (int i = tid; i < a.live; i += RB_THREADS) {
-            const int p = ph[i];
-            const int64_t n = (p >= 0 && p < a.old_len) ? rm[p] : -1;
-            if (n < 0) lost = 1;
-            ph[i] = (int32_t)n;
+        for (int i0 = 0; i0 < a.live; i0 += RM_THREADS * RM_BATCH) {
+            int p[RM_BATCH];
+            int64_t nw[RM_BATCH];
+#pragma unroll
+            for (int r = 0; r < RM_BATCH; ++r) {
+                const int i = i0 + r * RM_THREADS + tid;
+                p[r] = i < a.live ? ph[i] : -1;
+            }
+#pragma unroll
+            for (int r = 0; r < RM_BATCH; ++r) nw[r] = (p[r] >= 0 && p[r] < a.old_len) ? rm[p[r]] : -1;
+#pragma unroll
+            for (int r = 0; r < RM_BATCH; ++r) {
+                const int i = i0 + r * RM_THREADS + tid;
+                if (i < a.live) {
+                    if (nw[r] < 0) lost = 1;
+                    ph[i] = (int32_t)nw[r];
+                }
+            }
         }
     }
     if (bad) atomicOr(&flags, 1);
@@ -458,14 +489,21 @@ __device__ void stage_chunk(const RbArgs &a, const LaneStore &o, const LaneStore
     }
 }
 
-// grid: [remap: lanes] [copy: lanes x (g1 + g3)] [encode: lanes x g2] [stage: lanes x ceil(st/32)]
+// grid: [remap fill: lanes x nfill] [copy: lanes x (g1 + g3)] [encode: lanes x g2]
+// [stage: lanes x ceil(st/32)]; the remap itself follows in remap_kernel.
+constexpr int FILL_PER_BLOCK = RB_THREADS * 16;
+
 __global__ void __launch_bounds__(RB_THREADS) rebuild_kernel(RbArgs a) {
     int64_t idx = blockIdx.x;
-    if (idx < a.lanes) {
-        remap_lane(a, (int)idx);
+    const int nfill = (a.old_len + FILL_PER_BLOCK - 1) / FILL_PER_BLOCK;
+    if (idx < (int64_t)a.lanes * nfill) {
+        const int lane = (int)(idx / nfill), c = (int)(idx % nfill);
+        int64_t *rm = a.remap + lane * a.sremap;
+        const int end = min(a.old_len, (c + 1) * FILL_PER_BLOCK);
+        for (int i = c * FILL_PER_BLOCK + threadIdx.x; i < end; i += RB_THREADS) rm[i] = -1;
         return;
     }
-    idx -= a.lanes;
+    idx -= (int64_t)a.lanes * nfill;
     const int ncopy = a.g1 + a.g3, nstc = (a.st + KG - 1) / KG;
     int lane, kind, j;
     if (idx < (int64_t)a.lanes * ncopy) {
@@ -625,8 +663,10 @@ extern "C" int ma_rebuild_packed(const ma_prefix *old_store, int B, int H, int D
         ma_set_error("%s: NULL pointer", who);
         return MA_EINVAL;
     }
-    if ((g1 && gb_stride < g1) || (m && enc_stride < m) || (g3 && ga_stride < g3) || (st && stage_stride < st) ||
-        (old_len && remap_stride < old_len) || (live && phys_stride < live)) {
+    // a list's lane stride is its row length or more, or 0 (one list for every lane)
+    auto short_row = [](int64_t stride, int n) { return n && stride != 0 && stride < n; };
+    if (short_row(gb_stride, g1) || short_row(enc_stride, m) || short_row(ga_stride, g3) ||
+        short_row(stage_stride, st) || (old_len && remap_stride < old_len) || (live && phys_stride < live)) {
         ma_set_error("%s: a lane stride is shorter than its row", who);
         return MA_EINVAL;
     }
@@ -666,11 +706,16 @@ extern "C" int ma_rebuild_packed(const ma_prefix *old_store, int B, int H, int D
         ma_set_error("%s: key groups to copy but the old storage has none", who);
         return MA_EINVAL;
     }
-    const int64_t blocks = (int64_t)lanes * (1 + g1 + g3 + g2 + (st + KG - 1) / KG);
+    const int64_t nfill = (old_len + FILL_PER_BLOCK - 1) / FILL_PER_BLOCK;
+    const int64_t blocks = (int64_t)lanes * (nfill + g1 + g3 + g2 + (st + KG - 1) / KG);
     if (blocks > 0x7fffffff) {
         ma_set_error("%s: grid of %lld workgroups too large", who, (long long)blocks);
         return MA_EINVAL;
     }
-    hipLaunchKernelGGL(rebuild_kernel, dim3((unsigned)blocks), dim3(RB_THREADS), 0, (hipStream_t)stream, a);
+    if (blocks > 0)
+        hipLaunchKernelGGL(rebuild_kernel, dim3((unsigned)blocks), dim3(RB_THREADS), 0, (hipStream_t)stream, a);
+    rc = ma_check_launch(who);
+    if (rc) return rc;
+    hipLaunchKernelGGL(remap_kernel, dim3(lanes), dim3(RM_THREADS), 0, (hipStream_t)stream, a);
     return ma_check_launch(who);
 }

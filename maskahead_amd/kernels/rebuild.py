@@ -19,13 +19,23 @@ KG = 32
 
 
 def _lanes2d(t: torch.Tensor, name: str) -> torch.Tensor:
-    """[..., n] int64 index list -> contiguous [lanes, n]."""
+    """[..., n] int64 index list -> [lanes, n] with contiguous rows: a view when the lanes
+    are uniformly strided (a slice of a wider list, or one list broadcast to every lane,
+    lane stride 0), else a copy."""
     if t.dtype != torch.int64:
         raise ValueError(f"{name} must be int64")
     lanes = 1
     for x in t.shape[:-1]:
         lanes *= int(x)
-    return t.reshape(lanes, t.shape[-1]).contiguous()
+    t2 = t.reshape(lanes, t.shape[-1])
+    if t2.shape[1] > 1 and t2.stride(1) != 1:
+        t2 = t2.contiguous()
+    return t2
+
+
+def _stride(t2: torch.Tensor) -> int:
+    """Lane stride of a [lanes, n] list (0 for a single lane or a broadcast list)."""
+    return t2.stride(0) if t2.shape[0] > 1 else 0
 
 
 def rebuild_plan(phys: torch.Tensor, pos: torch.Tensor, live: int, *, quantized_length: int, need: int,
@@ -90,7 +100,7 @@ def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Ten
     if r2.shape[1] != old_len or r2.stride(-1) != 1 or remap.dtype != torch.int64:
         raise ValueError(f"remap must be int64 [lanes, {old_len}] with contiguous rows")
     dev = remap.device
-    status = torch.zeros((lanes,), device=dev, dtype=torch.int32)
+    status = torch.empty((lanes,), device=dev, dtype=torch.int32)   # written for every lane
     ph_ptr, ph_stride = None, 0
     if phys is not None and live:
         p2 = phys.reshape(lanes, -1)
@@ -100,8 +110,8 @@ def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Ten
     on, nn = old.native(), new.native()
     gb, enc, ga, stg = lists
     N.call("ma_rebuild_packed", ctypes.byref(on), B, H, D, ctypes.byref(nn),
-           gb.data_ptr(), gb.stride(0), gb.shape[1], enc.data_ptr(), enc.stride(0), enc.shape[1],
-           ga.data_ptr(), ga.stride(0), ga.shape[1], stg.data_ptr(), stg.stride(0), stg.shape[1],
+           gb.data_ptr(), _stride(gb), gb.shape[1], enc.data_ptr(), _stride(enc), enc.shape[1],
+           ga.data_ptr(), _stride(ga), ga.shape[1], stg.data_ptr(), _stride(stg), stg.shape[1],
            r2.data_ptr(), r2.stride(0), ph_ptr, ph_stride, int(live if ph_ptr else 0), status.data_ptr(),
            N.stream_of(remap))
     s = int(status.max()) if lanes else 0
