@@ -16,12 +16,16 @@ before timing.  The step is captured once in a HIP graph and replayed; the domin
 kernel (split-K pass 1) is also timed alone from its own graph.  Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--layers L] [--split-tokens S] [--no-cpu]
+
+--workload evict measures instead the packed lazy eviction of every layer (the rebuild
+that follows a keep-set selection); its JSON line names its own metric.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -51,6 +55,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall-clock budget of the CPU baseline sample (repeated whole steps)")
     ap.add_argument("--eager", action="store_true", help="also time the step without the HIP graph")
+    ap.add_argument("--workload", choices=("step0", "evict"), default="step0",
+                    help="step0: the headline read step (default); evict: the packed lazy eviction of all "
+                         "28 layers (state compaction, rebuild plan, rebuild)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="launch a plain 512 MiB device copy three times first, as the calibration "
                          "kernel of a FETCH_SIZE / WRITE_SIZE counter run")
@@ -149,6 +156,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
 
+    if a.workload == "evict":
+        bench_evict(a)
+        return
     from maskahead_amd import _native as N
     from maskahead_amd.kernels import (gather_packed_kv, prefix_scores, quantize_key_groups_into,
                                        quantize_values_into, splitk_attention, topk_ascending)
@@ -316,6 +326,185 @@ def main():
                                           f"median step",
                                 "cpu": platform.processor() or platform.machine(),
                                 "os_cpu_count": os.cpu_count()}
+    print(json.dumps(line), flush=True)
+
+
+def bench_evict(a):
+    """The packed lazy eviction of every layer (session.py:270-361 + cache.py:236-335):
+    28 layers x 4 KV heads of a 32 768-token int4 prefix + 32 bf16 residual tokens,
+    keep 4 096 per lane (a 128-token recency window + a clustered seeded score), repack
+    threshold 0.5.  A step = the eviction state's compaction, the rebuild plan and the
+    rebuild (two host synchronisations, as in the reference), timed one eviction at a
+    time from a restored cache.  The rebuild's two launches are also timed alone with
+    events over repeated launches on fixed lists (the roofline kernel)."""
+    from maskahead_amd import _native as N
+    from maskahead_amd.cache import PackedKVCache
+    from maskahead_amd.config import QuantizationConfig
+    from maskahead_amd.eviction import EvictionConfig, EvictionState
+    from maskahead_amd.kernels.rebuild import rebuild_packed, rebuild_plan
+    from maskahead_amd.kernels.splitk import Prefix
+    from maskahead_amd.runtime.session import evict_to
+
+    dev = torch.device("cuda:0")
+    L, B, H, D, N0, R, C, W, repack = a.layers, 1, 4, 128, 32768, 32, 4096, 128, 0.5
+    cache = PackedKVCache(num_layers=L, batch_size=B, num_kv_heads=H, head_dim=D, max_tokens=1 << 20,
+                          quant=QuantizationConfig(residual_tokens=R), device=dev)
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    cache.begin_append(N0 + R)
+    for li in range(L):
+        k = torch.randn((B, H, N0 + R, D), device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn((B, H, N0 + R, D), device=dev, generator=g).to(torch.bfloat16)
+        cache.stage_layer(li, k, v)
+    cache.commit_append()
+    n = cache.length
+    st = EvictionState(num_layers=L, batch_size=B, num_kv_heads=H, capacity=n, device=dev)
+    st.append(range(n))
+    gc = torch.Generator().manual_seed(1234)
+    score = torch.rand((L, B, H, n), generator=gc)
+    grp = torch.arange(n) // 32
+    for lane in range(L * B * H):
+        dense = torch.randperm(n // 32, generator=gc)[:20]
+        score[lane // (B * H), (lane // H) % B, lane % H] += 2.0 * torch.isin(grp, dense)
+    score[..., n - W:] = 1e9
+    keep = score.topk(C, dim=-1).indices.sort(dim=-1).values.to(dev)
+    names = ("k_q", "k_scale", "k_zero", "v_q", "v_scale", "v_zero", "k_residual", "v_residual")
+    saved = {x: getattr(cache, x) for x in names}
+    meta = ("length", "quantized_length", "residual_length", "dropped", "capacity", "residual_capacity")
+    saved_meta = {x: getattr(cache, x) for x in meta}
+    pos0, phys0 = st.pos.clone(), st.phys.clone()
+    cfg = EvictionConfig(policy="recent", recent_window=W, capacity_floor=W, compaction="lazy", repack_below=repack)
+
+    def restore():
+        for x in names:
+            setattr(cache, x, saved[x])
+        for x in meta:
+            setattr(cache, x, saved_meta[x])
+        st.pos.copy_(pos0)
+        st.phys.copy_(phys0)
+        st.live = n
+
+    times = []
+    for i in range(a.warmup + a.steps):
+        restore()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        evict_to(cache, st, keep, cfg, next_position=n)
+        torch.cuda.synchronize()
+        if i >= a.warmup:
+            times.append(time.perf_counter() - t0)
+    us = statistics.median(times) * 1e6
+    new_lens = (cache.length, cache.quantized_length, cache.residual_length)
+
+    # the rebuild alone: the lists of this eviction, fixed storage, repeated launches
+    restore()
+    st.compact(keep)
+    need = max(1, math.ceil(repack * 32))
+    gb, enc, stg = rebuild_plan(st.phys, st.pos, C, quantized_length=cache.quantized_length, need=need,
+                                tail_groups=0, window=min(W, C))
+    ga = torch.empty((L, B, H, 0), dtype=torch.int64, device=dev)
+    g1, m, nst = gb.shape[-1], enc.shape[-1], stg.shape[-1]
+    g2 = -(-m // 32)
+    ql = (g1 + g2) * 32
+    f = lambda t: t.flatten(0, 1)  # noqa: E731
+    kq = torch.empty((L, B, H, ql // 32, D, 16), dtype=torch.uint8, device=dev)
+    ks, kz = (torch.empty((L, B, H, ql // 32, D), dtype=torch.float16, device=dev) for _ in range(2))
+    vq = torch.empty((L, B, H, ql, D // 32, 16), dtype=torch.uint8, device=dev)
+    vs, vz = (torch.empty((L, B, H, ql, D // 32), dtype=torch.float16, device=dev) for _ in range(2))
+    kr, vr = (torch.empty((L, B, H, max(nst, 1), D), dtype=torch.bfloat16, device=dev) for _ in range(2))
+    old = Prefix(kq=f(cache.k_q), ks=f(cache.k_scale), kz=f(cache.k_zero), vq=f(cache.v_q), vs=f(cache.v_scale),
+                 vz=f(cache.v_zero), kf=f(cache.k_residual), vf=f(cache.v_residual), nq=cache.quantized_length,
+                 nf=cache.residual_length, kb=4, vb=4)
+    new = Prefix(kq=f(kq), ks=f(ks), kz=f(kz), vq=f(vq), vs=f(vs), vz=f(vz), kf=f(kr), vf=f(vr), nq=ql, nf=nst,
+                 kb=4, vb=4)
+    remap = torch.empty((L, B, H, n), dtype=torch.int64, device=dev)
+
+    def rebuild():
+        rebuild_packed(old, new, B=L * B, H=H, D=D, groups_before=gb, encode=enc, groups_after=ga, stage=stg,
+                       remap=remap)
+
+    for _ in range(3):
+        rebuild()
+    torch.cuda.synchronize()
+    inner = 20
+    cur = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    lib = N.load()
+    on, nn = old.native(), new.native()
+    status = torch.empty((L * B * H,), dtype=torch.int32, device=dev)
+    import ctypes
+
+    gb2, enc2, stg2 = (t.reshape(L * B * H, t.shape[-1]) for t in (gb, enc, stg))
+    args = (ctypes.byref(on), L * B, H, D, ctypes.byref(nn), gb2.data_ptr(), gb2.stride(0), g1, enc2.data_ptr(),
+            enc2.stride(0), m, None, 0, 0, stg2.data_ptr(), stg2.stride(0), nst, remap.data_ptr(), n, None, 0, 0,
+            status.data_ptr(), cur.cuda_stream)
+    e0.record(cur)
+    for _ in range(inner):
+        N.check(lib.ma_rebuild_packed(*args), "ma_rebuild_packed")
+    e1.record(cur)
+    torch.cuda.synchronize()
+    us_rebuild = e0.elapsed_time(e1) * 1e3 / inner
+
+    # algorithmic bytes of the rebuild launches (per lane, summed): kept groups read +
+    # written (5 120 B per group: K and V codes 2 x 2 048 B, scale / zero 2 x 512 B);
+    # encoded and staged entries read from the packed part (160 B: 64 B K codes + 64 B V
+    # codes + 16 + 16 B of scale / zero) or the bf16 residual (512 B); encoded entries
+    # written packed (160 B), staged ones bf16 (512 B); the remap written (8 B per old slot)
+    lanes = L * B * H
+    src = torch.cat([enc, stg], -1)
+    n_packed = int(((src >= 0) & (src < cache.quantized_length)).sum())
+    n_res = int((src >= cache.quantized_length).sum())
+    n_enc, n_stg = int((enc >= 0).sum()), int((stg >= 0).sum())
+    n_grp = int((gb >= 0).sum())
+    rb_bytes = (n_grp * 5120 * 2 + n_packed * 160 + n_res * 512 + n_enc * 160 + n_stg * 512 + lanes * n * 8
+                + lanes * (g1 * 32 + m + nst) * 8)
+    achieved = rb_bytes / (us_rebuild * 1e-6) / 1e9
+    line = {
+        "metric": "\u00b5s per packed lazy eviction of 28 layers (keep 4096 of 32800 per KV head, int4 KV)",
+        "value": round(us, 1),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes / bf16 requantization",
+        "data": "synthetic (seed 1234: N(0,1) K/V; clustered seeded keep score, 128-token window)",
+        "config": {"workload": f"evict_c4_k4v4_n32768: state compaction + rebuild plan + packed rebuild of "
+                               f"{L} layers x {H} KV heads, prefix {N0} int4 + {R} bf16, keep {C}, window {W}, "
+                               f"repack_below {repack}",
+                   "layers": L, "new_lengths": new_lens, "kept_groups": n_grp, "encoded": n_enc,
+                   "staged": n_stg},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "rebuild_kernel + remap_kernel", "avg_launch_us": round(us_rebuild, 2),
+                     "algorithmic_bytes": rb_bytes},
+    }
+    if not a.no_cpu:
+        from oracle import rebuild as OR
+
+        # bounded sample: 2 of the layers, the same lists, on the host
+        Ls = 2
+        store = {"kq": cache.k_q[:Ls].cpu(), "ks": cache.k_scale[:Ls].cpu(), "kz": cache.k_zero[:Ls].cpu(),
+                 "vq": cache.v_q[:Ls].cpu(), "vs": cache.v_scale[:Ls].cpu(), "vz": cache.v_zero[:Ls].cpu(),
+                 "kr": cache.k_residual[:Ls].cpu(), "vr": cache.v_residual[:Ls].cpu()}
+        lens = (cache.length, cache.quantized_length, cache.residual_length, cache.dropped)
+        pos, phys = pos0[:Ls, ..., :n].cpu().to(torch.int64), phys0[:Ls, ..., :n].cpu().to(torch.int64)
+        torch.set_num_threads(os.cpu_count() or 1)
+        ctimes = []
+        t_start = time.perf_counter()
+        while len(ctimes) < 2 or time.perf_counter() - t_start < min(a.cpu_seconds, 30.0):
+            t0 = time.perf_counter()
+            OR.evict(store, lens, pos, phys, keep[:Ls].cpu(), next_position=n, stage_mode=False, mode="lazy",
+                     repack_below=repack, recent_window=W)
+            ctimes.append(time.perf_counter() - t0)
+        per_evict = statistics.median(ctimes) * L / Ls
+        line["cpu_baseline"] = {"value": round(per_evict * 1e6, 1), "unit": "us", "cores": torch.get_num_threads(),
+                                "kind": "port",
+                                "sample": f"{len(ctimes)} evictions of {Ls} of the {L} layers (oracle/rebuild.py, "
+                                          f"torch CPU ops), median x {L // Ls}",
+                                "cpu": platform.processor() or platform.machine(), "os_cpu_count": os.cpu_count()}
     print(json.dumps(line), flush=True)
 
 
