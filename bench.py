@@ -55,9 +55,12 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall-clock budget of the CPU baseline sample (repeated whole steps)")
     ap.add_argument("--eager", action="store_true", help="also time the step without the HIP graph")
-    ap.add_argument("--workload", choices=("step0", "evict"), default="step0",
+    ap.add_argument("--workload", choices=("step0", "evict", "substep"), default="step0",
                     help="step0: the headline read step (default); evict: the packed lazy eviction of all "
-                         "28 layers (state compaction, rebuild plan, rebuild)")
+                         "28 layers (state compaction, rebuild plan, rebuild); substep: the denoising "
+                         "sub-step attention over [2048 selected | block] of 28 layers")
+    ap.add_argument("--block", type=int, default=32, help="substep: queries per block (32, or 8 for the "
+                                                          "Fast-dLLM block cache)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="launch a plain 512 MiB device copy three times first, as the calibration "
                          "kernel of a FETCH_SIZE / WRITE_SIZE counter run")
@@ -158,6 +161,9 @@ def main():
 
     if a.workload == "evict":
         bench_evict(a)
+        return
+    if a.workload == "substep":
+        bench_substep(a)
         return
     from maskahead_amd import _native as N
     from maskahead_amd.kernels import (gather_packed_kv, prefix_scores, quantize_key_groups_into,
@@ -326,6 +332,56 @@ def main():
                                           f"median step",
                                 "cpu": platform.processor() or platform.machine(),
                                 "os_cpu_count": os.cpu_count()}
+    print(json.dumps(line), flush=True)
+
+
+def bench_substep(a):
+    """A denoising sub-step of every layer (session.py:1286-1336; sdpa_compact,
+    reference.py:403-426): softmax attention of the block's queries over [the 2 048
+    entries selected at step 0 | the block's own K/V], per layer from that layer's compact
+    bf16 buffer, as runtime.fastpath.compact_attention runs it (split-K pass 1 + merge, no
+    copy of the block into the buffer).  28 layers per timed step in one HIP graph."""
+    from maskahead_amd.kernels import splitk_attention
+    from maskahead_amd.kernels.splitk import Prefix
+
+    dev = torch.device("cuda:0")
+    B, HQ, H, D, K, T = 1, 28, 4, 128, 2048, a.block
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    layers = []
+    for _ in range(a.layers):
+        ck = torch.randn((B, H, K + 32, D), device=dev, generator=g).to(torch.bfloat16)
+        cv = torch.randn((B, H, K + 32, D), device=dev, generator=g).to(torch.bfloat16)
+        layers.append(Prefix.dense(ck[:, :, :K], cv[:, :, :K]))
+    q = torch.randn((B, HQ, T, D), device=dev, generator=g).to(torch.bfloat16)
+    kc = torch.randn((B, H, T, D), device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn((B, H, T, D), device=dev, generator=g).to(torch.bfloat16)
+    scale = D ** -0.5
+
+    def step():
+        for pre in layers:
+            splitk_attention(q, pre, kc, vc, scaling=scale, split_tokens=a.split_tokens)
+
+    ms_step, _ = time_graph(step, a.steps, a.warmup)
+    us = ms_step * 1e3 / a.layers
+    R = (HQ // H) * T
+    nbytes = H * (K + T) * D * 2 * 2 + 2 * B * HQ * T * D * 2      # K, V read; Q read, out written
+    flops = 4 * R * (K + T) * D * H
+    t = us * 1e-6
+    f_hbm = nbytes / t / 1e9 / HBM_PEAK_GBS
+    f_mfma = flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    line = {
+        "metric": f"\u00b5s per layer sub-step (attention over [2048 selected | {T}-token block], bf16 compact)",
+        "value": round(us, 3), "unit": "us", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seed 1234: N(0,1) compact K/V, queries, block K/V)",
+        "config": {"workload": f"substep_k2048_t{T}: B{B} Hq{HQ} Hkv{H} D{D}, {a.layers} layers per graph replay",
+                   "split_tokens": a.split_tokens or "auto", "algorithmic_bytes": nbytes, "algorithmic_flops": flops},
+        "roofline": {"bound": "hbm" if nbytes / HBM_PEAK_GBS / 1e9 >= flops / MFMA_BF16_PEAK_TFLOPS / 1e12 else "mfma",
+                     "achieved": round(nbytes / t / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(f_hbm, 4), "traffic": None, "kernel": "splitk_fwd_kernel<128, 1> + "
+                     "splitk_combine_kernel<128> (whole sub-step)", "avg_launch_us": round(us, 3),
+                     "mfma_frac": round(f_mfma, 4)},
+    }
     print(json.dumps(line), flush=True)
 
 

@@ -729,7 +729,10 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
 
 // Tokens per split: about one workgroup per CU (one 133 KB-LDS workgroup fits a CU), with
 // one CU per (lane, row group) left for the current block's workgroups, so every
-// workgroup of the launch runs in the first dispatch wave; never below 256 tokens.
+// workgroup of the launch runs in the first dispatch wave; at least one 64-token tile.
+// Short prefixes (a sub-step's 2 048 selected entries) thus spread over many CUs: each
+// workgroup's cost is mostly fixed latency, so more, shorter splits finish sooner
+// (22.1 -> 17.9 us per sub-step at 4 KV heads x 2 048 entries, measured).
 int choose_split(int n, int BH, int row_groups, int split_tokens) {
     if (split_tokens > 0) return split_tokens;
     const int units = BH * row_groups;
@@ -737,7 +740,7 @@ int choose_split(int n, int BH, int row_groups, int split_tokens) {
     if (per < 1) per = 1;
     int sn = (n + per - 1) / per;
     sn = ((sn + TILE - 1) / TILE) * TILE;
-    if (sn < 256) sn = 256;
+    if (sn < TILE) sn = TILE;
     return sn;
 }
 
