@@ -108,6 +108,8 @@ class FastLayerPath:
     slot_masks: dict = field(default_factory=dict)
     states: dict = field(default_factory=dict)
     last_mass: dict = field(default_factory=dict)
+    probe_mass: dict = field(default_factory=dict)
+    chunk_mass: dict = field(default_factory=dict)
     _rows_cache: tuple | None = None
 
     @property
@@ -149,6 +151,39 @@ class FastLayerPath:
         rows = mass_rows if isinstance(mass_rows, torch.Tensor) else self.rows(mass_rows)
         mass, _ = prefix_scores(query, prefix, stats, rows, value=False, scaling=self.head_dim ** -0.5)
         return out, mass
+
+    def probe(self, layer_idx, query, current_key, current_value, *, live_slots=None):
+        """A lookahead probe forward on the fast path (session.py:2317-2332): the masked
+        blocks k+1 .. k+M in one forward, block-causal over [live prefix | blocks] (block j
+        reads blocks <= j).  The prefix mass of the queries of blocks k+2 .. (block
+        positions block_size .. t-1) times the number of those blocks goes to
+        probe_mass[layer_idx], in live order when live_slots [B, Hkv, live] (the eviction
+        state's slots) is given (session.py:257-261)."""
+        b = self.block_size
+        t = query.shape[2]
+        rows = list(range(b, t))
+        out, mass = self.attend(layer_idx, query, current_key, current_value, causal=b, q_pos0=0,
+                                mass_rows=rows if rows else None)
+        if mass is not None:
+            if live_slots is not None:
+                mass = mass.gather(-1, live_slots.to(torch.int64))
+            self.probe_mass[layer_idx] = mass * max(1, (t - b) // b)
+        return out
+
+    def prefill_chunk(self, layer_idx, query, current_key, current_value, *, want_mass: bool = False,
+                      live_slots=None):
+        """A prefill chunk on the fast path (session.py:1827-1876): block-causal attention
+        over [live prefix | chunk]; with want_mass the prefix mass of every chunk position
+        goes to chunk_mass[layer_idx] (live order when live_slots is given), the input of
+        the EMA and chunk-wise lookahead policies."""
+        t = query.shape[2]
+        out, mass = self.attend(layer_idx, query, current_key, current_value, causal=self.block_size, q_pos0=0,
+                                mass_rows=list(range(t)) if want_mass else None)
+        if mass is not None:
+            if live_slots is not None:
+                mass = mass.gather(-1, live_slots.to(torch.int64))
+            self.chunk_mass[layer_idx] = mass
+        return out
 
     def ensure_state(self, layer_idx: int, selected_k: int) -> CompactLayerState:
         """session.py:438-454."""

@@ -8,7 +8,10 @@ blocks (runtime/session.py:27-40).  Here it runs in the gfx950 kernels of
 
 ``evict_to`` is the session's eviction step (session.py:270-361): the eviction state's
 compaction, then the lazy / full rebuild of a packed cache (ma_rebuild_plan,
-ma_rebuild_packed) or the exact compaction of a 16-bit one.
+ma_rebuild_packed) or the exact compaction of a 16-bit one.  ``lookahead_evict``
+(session.py:1985-2034) scores the live entries with the step-0 and probe masses and
+evicts to the budget; ``live_slot_masks`` (session.py:240-255) gives the attention
+kernels the live slots of a cache that keeps dead slots after a lazy rebuild.
 """
 
 from __future__ import annotations
@@ -81,3 +84,56 @@ def evict_to(cache, state, keep: torch.Tensor, cfg, *, next_position: int, phys_
     else:
         groups_after = empty
     cache._rebuild(groups_before, enc_slots, groups_after, stage_slots, phys=state.phys, live=live)
+
+
+def live_slot_masks(cache, state) -> dict:
+    """uint8 [B, Hkv, cache.length] per layer, 1 on the live slots (session.py:240-255);
+    empty when every stored slot is live.  Pass it as FastLayerPath.slot_masks."""
+    live = state.live
+    if cache.length <= live:
+        return {}
+    out = {}
+    for layer in range(state.num_layers):
+        m = torch.zeros((cache.batch_size, cache.num_kv_heads, cache.length), dtype=torch.uint8, device=cache.device)
+        m.scatter_(-1, state.phys[layer, ..., :live].to(torch.int64), 1)
+        out[layer] = m
+    return out
+
+
+def live_values(cache, state, layer_idx: int) -> torch.Tensor:
+    """Values of the live entries of one layer, [B, Hkv, live, D] in the compute dtype
+    (session.py:263-268), gathered from the packed or 16-bit cache by ma_gather_kv."""
+    from ..kernels.ops import gather_packed_kv
+
+    slots = state.phys[layer_idx, ..., :state.live].to(torch.int64)
+    _, v = gather_packed_kv(cache.layer_view(layer_idx), slots, dtype=cache.compute_dtype)
+    return v
+
+
+def lookahead_scores(cache, state, a1: dict, a_probe: dict | None = None, *, use_value: bool = True) -> torch.Tensor:
+    """score [L, B, Hkv, live] of the lookahead policy for layers on the fast path
+    (session.py:1995-2025): a = the step-0 mass of the block's own queries (a1[layer],
+    live order) + the probe mass of the next blocks (a_probe[layer], when probed); the
+    score is value_score(a, v_live) (lookahead_score "value") or a itself ("mass")."""
+    L = state.num_layers
+    score = torch.empty((L, cache.batch_size, cache.num_kv_heads, state.live), dtype=torch.float32,
+                        device=cache.device)
+    for layer in range(L):
+        a = a1[layer]
+        if a_probe is not None and layer in a_probe:
+            a = a + a_probe[layer]
+        score[layer] = value_score(a, live_values(cache, state, layer)) if use_value else a
+    return score
+
+
+def lookahead_evict(cache, state, cfg, capacity: int, a1: dict, a_probe: dict | None = None, *,
+                    next_position: int, phys_compact: bool = True):
+    """Evict to `capacity` with the lookahead score (session.py:1985-2034): the survivors
+    of the eviction state (ma_keep_select) under that score, then evict_to.  Returns the
+    keep set, or None when the live set already fits."""
+    if state.live <= capacity:
+        return None
+    score = lookahead_scores(cache, state, a1, a_probe, use_value=cfg.lookahead_score != "mass")
+    keep = state.survivors(cfg, capacity, None, score)
+    evict_to(cache, state, keep, cfg, next_position=next_position, phys_compact=phys_compact)
+    return keep
