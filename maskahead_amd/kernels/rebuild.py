@@ -114,7 +114,7 @@ def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Ten
            ga.data_ptr(), _stride(ga), ga.shape[1], stg.data_ptr(), _stride(stg), stg.shape[1],
            r2.data_ptr(), r2.stride(0), ph_ptr, ph_stride, int(live if ph_ptr else 0), status.data_ptr(),
            N.stream_of(remap))
-    s = int(status.max()) if lanes else 0
+    s = int(status.cpu().max()) if lanes else 0   # one small copy, no reduction kernel
     if s & 1:
         raise RuntimeError("rebuild: an index list names a slot or key group outside the cache")
     if s & 2:
