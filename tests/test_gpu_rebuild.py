@@ -176,3 +176,32 @@ def test_rebuild_direct_lists_and_errors(gpu):
     with pytest.raises(RuntimeError):
         cache.rebuild(gb.to(gpu), torch.tensor([[5, 144, -1], [1, 2, 3]]).view(1, 1, 2, 3).to(gpu), ga.to(gpu),
                       stg.to(gpu))
+
+
+def test_evict_to_bf16_cache_with_tail(gpu):
+    """A 16-bit cache (session.py:292-296): the live slots, then a stored-but-unadmitted
+    tail, gathered exactly in place; the state's slots become 0 .. live - 1."""
+    from maskahead_amd.config import QuantizationConfig as QC
+
+    L, H, D, n, tail, C = 2, 4, 64, 600, 40, 200
+    g = torch.Generator().manual_seed(77)
+    cache = PackedKVCache(num_layers=L, batch_size=1, num_kv_heads=H, head_dim=D, max_tokens=4096,
+                          quant=QC(k_bits=16, v_bits=16), device=gpu)
+    k = torch.randn((L, 1, H, n + tail, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((L, 1, H, n + tail, D), generator=g).to(torch.bfloat16)
+    cache.begin_append(n + tail)
+    for layer in range(L):
+        cache.stage_layer(layer, k[layer].to(gpu), v[layer].to(gpu))
+    cache.commit_append()
+    st = EvictionState(num_layers=L, batch_size=1, num_kv_heads=H, capacity=n, device=gpu)
+    st.append(range(n))
+    keep = torch.stack([torch.randperm(n, generator=g)[:C].sort().values for _ in range(L * H)]).view(L, 1, H, C)
+    cfg = EvictionConfig(policy="recent", recent_window=16, capacity_floor=16)
+    evict_to(cache, st, keep.to(gpu), cfg, next_position=n)
+    torch.cuda.synchronize()
+    src = torch.cat([keep, torch.arange(n, n + tail).expand(L, 1, H, tail)], -1)
+    gi = src.unsqueeze(-1).expand(-1, -1, -1, -1, D)
+    assert cache.length == C + tail and cache.dropped == n - C
+    assert same_bits(cache.k_fp[:, :, :, :C + tail], k.gather(3, gi))
+    assert same_bits(cache.v_fp[:, :, :, :C + tail], v.gather(3, gi))
+    assert torch.equal(st.phys[..., :C].cpu(), torch.arange(C, dtype=torch.int32).expand(L, 1, H, C))
