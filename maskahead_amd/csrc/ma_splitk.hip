@@ -583,21 +583,24 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         f32x16_t acc[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-        // prologue: K tiles 0 and 1 staged (their loads issued together, into two register
-        // sets), K tile 2 and V tile 0 in flight
+        // prologue: the loads of K tiles 0 and 1 issued together (two register sets) and V
+        // tile 0 in flight; K tile 0 staged before the first barrier, K tile 1 (buffer 1)
+        // while the S waves compute S^T of tile 0 from buffer 0, then K tile 2 in flight
+        StageRegs<Shape::NW> pr1;
+        pr1.flags = 0;
         if (is_k) {
-            StageRegs<Shape::NW> pr1;
-            pr1.flags = 0;
             if (nt > 0) load_k(0);
             if (nt > 1) load_k_into(pr1, 1);
             if (nt > 0) store_k(S.kt[0].k, S.kmask[0]);
-            if (nt > 1) store_k_from(pr1, S.kt[1].k, S.kmask[1]);
-            if (nt > 2) load_k(2);
         } else if (is_v && nt > 0) {
             load_v(0);
         }
         __syncthreads();
-        __syncthreads();  // the S waves have read K tile 0 out of buffer 0
+        if (is_k) {
+            if (nt > 1) store_k_from(pr1, S.kt[1].k, S.kmask[1]);
+            if (nt > 2) load_k(2);
+        }
+        __syncthreads();  // the S waves have read K tile 0 out of buffer 0; K tile 1 is staged
         for (int it = 0; it <= nt; ++it) {
             const int cb = it & 1, pb = cb ^ 1;
             if (is_o && it >= 1)
