@@ -382,6 +382,27 @@ def bench_substep(a):
                      "splitk_combine_kernel<128> (whole sub-step)", "avg_launch_us": round(us, 3),
                      "mfma_frac": round(f_mfma, 4)},
     }
+    if not a.no_cpu:
+        from oracle import attention as OA
+
+        # the reference's CPU sub-step (sdpa_compact, reference.py:403-426, restated in
+        # oracle.attention.dense_attention) on the first layer's compact buffer, repeated
+        pre0 = layers[0]
+        args = (q.cpu(), pre0.kf.cpu(), pre0.vf.cpu(), kc.cpu(), vc.cpu())
+        torch.set_num_threads(os.cpu_count() or 1)
+        OA.dense_attention(*args)
+        ctimes = []
+        t_start = time.perf_counter()
+        while len(ctimes) < 3 or time.perf_counter() - t_start < min(a.cpu_seconds, 10.0):
+            t0 = time.perf_counter()
+            OA.dense_attention(*args)
+            ctimes.append(time.perf_counter() - t0)
+        sec = statistics.median(ctimes)
+        line["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us", "cores": torch.get_num_threads(),
+                                "kind": "port",
+                                "sample": f"{len(ctimes)} layer sub-steps (oracle dense_attention over [2048 | {T}], "
+                                          "float64 torch ops) after 1 warm-up; median",
+                                "cpu": platform.processor() or platform.machine(), "os_cpu_count": os.cpu_count()}
     print(json.dumps(line), flush=True)
 
 
