@@ -111,6 +111,21 @@ int ma_splitk_attention(ma_tensor4 q, int B, int Hq, int T, int D, const ma_pref
                         int c_pos0, float scale, ma_tensor4 out, float *mp, float *lp, void *op,
                         int split_tokens, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference: ma_splitk_attention for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as ma_splitk_attention, without the workspace: the split
+ * partials live in a fixed library-owned device array of ma_splitk_noalloc_max_bytes()
+ * bytes (32 MiB) per device, held until the process ends.  A call whose
+ * ma_splitk_workspace_bytes() exceeds it returns MA_EWORKSPACE.  The call allocates
+ * nothing; the first call on a device looks up that device's copy of the array.  All calls
+ * on one device share the array, so calls that overlap in time on one device (two streams,
+ * two host threads) race; order them on one stream. */
+int64_t ma_splitk_noalloc_max_bytes(void);
+int ma_splitk_attention_noalloc(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
+                                ma_tensor4 kc, ma_tensor4 vc, int Tc, int causal_block, int q_pos0,
+                                int c_pos0, float scale, ma_tensor4 out, float *mp, float *lp, void *op,
+                                int split_tokens, void *stream);
+
 /* a6 (centre). The value centre of prefix_scores (splitk.py:599-601):
  * centre[b,h,:] = mean over g < G, t in q_rows of f32(op[b,h,g*T+t,:]); op dtype op_dtype. */
 int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, int D,

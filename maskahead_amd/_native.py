@@ -64,6 +64,9 @@ SIGNATURES = {
     "ma_splitk_partial": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _T4, _T4, _I, _I, _I, _I, _F, _I, _P, _I64, _P]),
     "ma_splitk_merge": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _T4, _T4, _I, _I, _I, _I, _F, _T4, _P, _P, _P, _I, _P,
                              _I64, _P]),
+    "ma_splitk_noalloc_max_bytes": (_I64, []),
+    "ma_splitk_attention_noalloc": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _T4, _T4, _I, _I, _I, _I, _F, _T4,
+                                         _P, _P, _P, _I, _P]),
     "ma_value_centre": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P]),
     "ma_prefix_scores": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _P, _I, _P, _P, _P, _I, _F, _I, _I, _P,
                               _P, _P]),

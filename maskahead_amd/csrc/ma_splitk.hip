@@ -20,6 +20,7 @@
 // fit 4 per SIMD and the MFMA work of one wave overlaps the VALU work of the others.
 // Pass 2 (splitk_combine_kernel): log-sum-exp merge of the partials into the output and
 // the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
+#include <mutex>
 #include <type_traits>
 
 #include "ma_stage.h"
@@ -937,6 +938,79 @@ extern "C" int ma_splitk_attention(ma_tensor4 q, int B, int Hq, int T, int D, co
     Plan pl;
     int rc = make_plan(pl, "ma_splitk_attention", q, B, Hq, T, D, p, H, kc, vc, Tc, causal_block, q_pos0, c_pos0,
                        scale, split_tokens, workspace, workspace_bytes);
+    if (rc) return rc;
+    rc = launch_partial(pl, (hipStream_t)stream);
+    if (rc) return rc;
+    return launch_merge(pl, out, mp, lp, op, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// ma_splitk_attention with its split partials in a library-owned device array instead of a
+// caller workspace, for callers that cannot allocate (code under HIP graph capture, tight
+// serving loops).  The array is a file-scope __device__ symbol: each device the library
+// runs on holds its own copy, at its own address, until the process ends.  Its device
+// address is looked up once per device with hipGetSymbolAddress (the symbol's name in host
+// code is only a host-side stand-in, never a device pointer) and that address is what the
+// kernels receive.  Nothing in the partials needs clearing: pass 1 writes every slot the
+// merge reads.  Calls that overlap in time on one device share the array and race.
+namespace {
+
+constexpr int64_t NOALLOC_SCRATCH_BYTES = 32ll << 20;
+__device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// the device address of `scratch` on the current device (looked up on the first call)
+int scratch_address(void **out, const char *who) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+        ma_set_error("%s: no current device (%s)", who, e != hipSuccess ? hipGetErrorString(e) : "out of range");
+        return MA_EHIP;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            ma_set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                         hipGetErrorString(e));
+            return MA_EHIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MA_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t ma_splitk_noalloc_max_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int ma_splitk_attention_noalloc(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
+                                           ma_tensor4 kc, ma_tensor4 vc, int Tc, int causal_block, int q_pos0,
+                                           int c_pos0, float scale, ma_tensor4 out, float *mp, float *lp, void *op,
+                                           int split_tokens, void *stream) {
+    const char *who = "ma_splitk_attention_noalloc";
+    const int64_t need = p ? ma_splitk_workspace_bytes(B, H, Hq, T, D, p->nq, p->nf, split_tokens) : -1;
+    if (need < 0) {
+        ma_set_error("%s: bad geometry (B=%d H=%d Hq=%d T=%d D=%d)", who, B, H, Hq, T, D);
+        return MA_EINVAL;
+    }
+    if (need > NOALLOC_SCRATCH_BYTES) {
+        ma_set_error("%s: this call needs %lld bytes of split partials, above the library's fixed %lld-byte "
+                     "scratch; use ma_splitk_attention with a workspace",
+                     who, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+        return MA_EWORKSPACE;
+    }
+    void *ws = nullptr;
+    int rc = scratch_address(&ws, who);
+    if (rc) return rc;
+    Plan pl;
+    rc = make_plan(pl, who, q, B, Hq, T, D, p, H, kc, vc, Tc, causal_block, q_pos0, c_pos0, scale, split_tokens, ws,
+                   NOALLOC_SCRATCH_BYTES);
     if (rc) return rc;
     rc = launch_partial(pl, (hipStream_t)stream);
     if (rc) return rc;
