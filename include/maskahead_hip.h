@@ -136,11 +136,14 @@ int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, in
  * slots) and, when value != 0, score[j] = mass[j] * ||v_j - centre|| (0 on dead slots),
  * centre as ma_value_centre computes it from op (the prefix-only output of
  * ma_splitk_attention, [B,H,R,D] contiguous, dtype op_dtype; read only when value != 0).
- * v_round_bf16: the distance reads V rounded to bf16 (the reference reads its unpacked
- * bf16 prefix when it has one, splitk.py:513-516, 592).  mass/score [B,H,n] contiguous. */
+ * v_round: 0, or MA_BF16 / MA_F16: the distance reads packed V rounded to that dtype (the
+ * reference reads the prefix it unpacked to the query dtype when it has one,
+ * splitk.py:513-516, 592).  mass/score [B,H,n] contiguous.  Mass-only calls take any number
+ * of selection rows (run in passes of at most 512, each adding its share of the mean);
+ * value-aware calls take at most 512 selection rows and 1 024 rows per KV head. */
 int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
                      const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
-                     int op_dtype, float scale, int value, int v_round_bf16, float *mass, float *score,
+                     int op_dtype, float scale, int value, int v_round, float *mass, float *score,
                      void *stream);
 
 /* a9. read-set top-k (session.py:1429-1438, reference.py:369-393): for each of `rows`

@@ -46,7 +46,10 @@ struct ScoreArgs {
     const void *op;  // prefix-only output [B*H, R, D] (op_dtype): the value centre's source
     int op_dtype;
     float *mass, *score;
-    int H, G, T, T2, R, R2, row_tiles, value, vround;
+    int H, G, T, T2, R, R2, row_tiles, value;
+    int vround;    // 0, or MA_BF16 / MA_F16: packed values rounded to that dtype for the distance
+    int r2_total;  // selection rows of the whole call (the mean's divisor) when rows run in passes
+    int accum;     // this pass adds its share to mass (passes after the first; mass only)
     int nfast;     // whole tiles of the source kind per lane: tiles [0, nfast)
     int per;       // tiles per fast workgroup
     int fast_wgs;  // fast workgroups per lane (blockIdx.x below it); then one tail tile each
@@ -181,8 +184,9 @@ __device__ __forceinline__ void vp_load(uint32_t *w, const uint8_t *vq, const ui
 }
 
 // squared distance of the item's 16 channels to the centre (cen16: those channels, LDS);
-// VR: the values are rounded to bf16 first (the reference's unpacked bf16 prefix)
-template <bool VR>
+// VR: the values are first rounded to the dtype (MA_BF16 / MA_F16) of the reference's
+// unpacked prefix, 0 = read as dequantized (f32)
+template <int VR>
 __device__ __forceinline__ float vp_dist(const uint32_t *w, const float *cen16) {
     const float s = ma_f16_to_f32(w[2] & 0xffff), z = ma_f16_to_f32(w[2] >> 16);
     float q[16];
@@ -195,10 +199,13 @@ __device__ __forceinline__ float vp_dist(const uint32_t *w, const float *cen16) 
 #pragma unroll
         for (int e = 0; e < 4; e += 2) {
             float x0 = __builtin_fmaf(q[c4 * 4 + e], s, z), x1 = __builtin_fmaf(q[c4 * 4 + e + 1], s, z);
-            if constexpr (VR) {
+            if constexpr (VR == MA_BF16) {
                 const uint32_t pk = ma_pack_bf16x2(x0, x1);
                 x0 = __uint_as_float(pk << 16);
                 x1 = __uint_as_float(pk & 0xffff0000u);
+            } else if constexpr (VR == MA_F16) {
+                x0 = ma_round_f16(x0);
+                x1 = ma_round_f16(x1);
             }
             const float d0 = x0 - cc[e], d1 = x1 - cc[e + 1];
             acc = __builtin_fmaf(d0, d0, acc);
@@ -237,7 +244,7 @@ __device__ __forceinline__ float vd_dist(const uint32_t *w, const float *cen16, 
 
 // element-wise V distance of item u (any prefix kind; f32 prefixes keep f32 values)
 template <int D>
-__device__ __forceinline__ float vg_dist(const Lane &L, int u, int n0, int end, const float *cen16, bool vround) {
+__device__ __forceinline__ float vg_dist(const Lane &L, int u, int n0, int end, const float *cen16, int vround) {
     const int t = u / (D / 16), c0 = (u % (D / 16)) * 16;
     const int j = n0 + t;
     float acc = 0.f;
@@ -245,7 +252,7 @@ __device__ __forceinline__ float vg_dist(const Lane &L, int u, int n0, int end, 
 #pragma unroll 2
         for (int c = 0; c < 16; ++c) {
             float x = lane_value(L, j, c0 + c);
-            if (vround && j < L.nq) x = ma_round_bf16(x);
+            if (j < L.nq) x = vround == MA_BF16 ? ma_round_bf16(x) : vround == MA_F16 ? ma_round_f16(x) : x;
             const float dl = x - cen16[c];
             acc = __builtin_fmaf(dl, dl, acc);
         }
@@ -356,13 +363,19 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
     // the selection-row tables from LDS, then Q and the value centre
     if (fast) load(0);
     if (tid < T2) sm.qr[tid] = a.q_rows[tid];
-    for (int r = tid; r < R; r += SNT) {
+    // exp(s - M) / L == exp2(s*log2e - (M*log2e + log2 L)); rows without a live prefix
+    // entry (L = 0) and padding rows contribute exactly 0.  Up to MAX_R rows per KV head the
+    // constants of every row come in the same round trip as q_rows; beyond (long prefill
+    // chunks, mass only) each selection row reads its own M_p / L_p below.
+    const bool row_table = R <= MAX_R;
+    auto row_const = [&](int r) {
         const float m = a.mp[(int64_t)bh * R + r], l = a.lp[(int64_t)bh * R + r];
-        // exp(s - M) / L == exp2(s*log2e - (M*log2e + log2 L)); rows without a live prefix
-        // entry (L = 0) and padding rows contribute exactly 0
-        sm.rowc[r] = l > 0.f ? __builtin_fmaf(m, MA_LOG2E, __log2f(l)) : __builtin_inff();
+        return l > 0.f ? __builtin_fmaf(m, MA_LOG2E, __log2f(l)) : __builtin_inff();
+    };
+    if (row_table) {
+        for (int r = tid; r < R; r += SNT) sm.rowc[r] = row_const(r);
+        for (int r = tid; r < MAX_R; r += SNT) sm.cnt[r] = 0;
     }
-    for (int r = tid; r < MAX_R; r += SNT) sm.cnt[r] = 0;
     __syncthreads();
     const int rt_pad = 32 * row_tiles;
     for (int rr = tid; rr < rt_pad; rr += SNT) {
@@ -373,8 +386,12 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
             const int t = min(max(sm.qr[rr - g * T2], 0), T - 1);   // as sel_row
             row = g * T + t;
             qo = g * (int)a.q.s[1] + t * (int)a.q.s[2];
-            atomicAdd(&sm.cnt[row], 1);
-            c = sm.rowc[row];
+            if (row_table) {
+                atomicAdd(&sm.cnt[row], 1);
+                c = sm.rowc[row];
+            } else {
+                c = row_const(row);
+            }
         }
         sm.crow[rr] = c;
         sm.rrow[rr] = row;
@@ -472,7 +489,7 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
         }
     };
 
-    const float inv_r2 = 1.0f / (float)R2;
+    const float inv_r2 = 1.0f / (float)a.r2_total;
     auto finish = [&](int tile, int rb, int db) {
         const int j = tile * TILE + lane;
         if (j < end) {
@@ -482,7 +499,8 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
             bool live = true;
             if (a.pre.mask) live = a.pre.mask[(int64_t)bh * end + j] != 0;
             const float m = live ? s * inv_r2 : 0.f;
-            a.mass[(int64_t)bh * end + j] = m;
+            if (a.accum) a.mass[(int64_t)bh * end + j] += m;
+            else a.mass[(int64_t)bh * end + j] = m;
             if (value) a.score[(int64_t)bh * end + j] = live ? m * __builtin_sqrtf(sm.dist[db][lane]) : 0.f;
         }
     };
@@ -514,7 +532,7 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
 
     // ---- fast workgroup: this thread's item of the tile in w into K buffer kb and
     // distance buffer db
-    const bool vround = a.vround;
+    const int vround = a.vround;
     const float *cen16 = &sm.cen[(has_item && tid >= NIK ? (tid - NIK) % TPI : 0) * 16];
     auto stage = [&](int kb, int db) {
         uint16_t *Ks = sm.u.kt[kb].k;
@@ -523,7 +541,9 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
             else kd_store<D>(Ks, w, tid, a.pre.fdtype);
         } else if (value && tid < NIK + NIK) {
             float dd = 0.f;
-            if constexpr (SRC == SRC_PACKED) dd = vround ? vp_dist<true>(w, cen16) : vp_dist<false>(w, cen16);
+            if constexpr (SRC == SRC_PACKED)
+                dd = vround == MA_BF16 ? vp_dist<MA_BF16>(w, cen16)
+                                       : (vround == MA_F16 ? vp_dist<MA_F16>(w, cen16) : vp_dist<0>(w, cen16));
             else dd = vd_dist(w, cen16, a.pre.fdtype);
             dd = token_sum<D>(dd);
             if ((tid - NIK) % TPI == 0) sm.dist[db][(tid - NIK) / TPI] = dd;
@@ -626,7 +646,7 @@ extern "C" int ma_value_centre(const void *op, int op_dtype, int B, int H, int G
 
 extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
                                 const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
-                                int op_dtype, float scale, int value, int v_round_bf16, float *mass, float *score,
+                                int op_dtype, float scale, int value, int v_round, float *mass, float *score,
                                 void *stream) {
     const char *who = "ma_prefix_scores";
     int rc = ma_validate_prefix(p, D, who);
@@ -646,12 +666,19 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
         return MA_EINVAL;
     }
     const int G = Hq / H, R = G * T, R2 = G * T2;
-    const int row_tiles = (R2 + 31) / 32;
-    if (row_tiles > MAX_RT || R > MAX_R) {
-        ma_set_error("%s: %d selection rows / %d rows per KV head exceed the built maximum %d / %d", who, R2, R,
-                     MAX_R2, MAX_R);
+    if (value && ((R2 + 31) / 32 > MAX_RT || R > MAX_R)) {
+        // the value score's centre is built in LDS over all rows of the KV head
+        ma_set_error("%s: value-aware scores of %d selection rows / %d rows per KV head exceed the built maximum "
+                     "%d / %d", who, R2, R, MAX_R2, MAX_R);
         return MA_EUNSUPPORTED;
     }
+    if (G > MAX_R2) {
+        ma_set_error("%s: %d query heads per KV head exceed the built maximum %d", who, G, MAX_R2);
+        return MA_EUNSUPPORTED;
+    }
+    // mass only: the selection rows in passes of at most MAX_R2 rows (whole q_rows entries),
+    // each adding its share of the mean to mass
+    const int t2_pass = value ? T2 : (MAX_R2 / G < T2 ? MAX_R2 / G : T2);
     const int n = p->nq + p->nf;
     if (n == 0) return MA_OK;
     // 16-bit parts are read with 32-byte vector loads: every token row must stay aligned
@@ -659,7 +686,8 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
                                              ((uintptr_t)p->kf & 15) == 0 && ((uintptr_t)p->vf & 15) == 0 &&
                                              p->skf[0] % 16 == 0 && p->skf[1] % 16 == 0 && p->svf[0] % 16 == 0 &&
                                              p->svf[1] % 16 == 0);
-    const int halves = row_tiles <= 8 ? 1 : 2;
+    const int row_tiles_max = (G * t2_pass + 31) / 32;
+    const int halves = row_tiles_max <= 8 ? 1 : 2;
     const int tiles = (n + TILE - 1) / TILE;
     const bool packed = p->nq > 0;
     // whole tiles of the source kind go to the pipelined workgroups, the rest (a tile
@@ -683,12 +711,14 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     sa.H = H;
     sa.G = G;
     sa.T = T;
-    sa.T2 = T2;
     sa.R = R;
-    sa.R2 = R2;
-    sa.row_tiles = row_tiles;
+    sa.r2_total = R2;
     sa.value = value;
-    sa.vround = v_round_bf16;
+    if (v_round != 0 && v_round != MA_BF16 && v_round != MA_F16) {
+        ma_set_error("%s: v_round must be 0, MA_BF16 or MA_F16", who);
+        return MA_EINVAL;
+    }
+    sa.vround = v_round;
     sa.nfast = nfast;
     sa.per = per;
     sa.fast_wgs = fast_wgs;
@@ -702,14 +732,24 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
         if (halves == 1) MA_SCORE(D_, S_, 1);     \
         else MA_SCORE(D_, S_, 2);                 \
     } while (0)
-    if (D == 128) {
-        if (packed) MA_SCORE_I(128, SRC_PACKED);
-        else MA_SCORE_I(128, SRC_DENSE);
-    } else {
-        if (packed) MA_SCORE_I(64, SRC_PACKED);
-        else MA_SCORE_I(64, SRC_DENSE);
+    for (int t0 = 0; t0 < T2; t0 += t2_pass) {
+        const int t2 = T2 - t0 < t2_pass ? T2 - t0 : t2_pass;
+        sa.q_rows = q_rows + t0;
+        sa.T2 = t2;
+        sa.R2 = G * t2;
+        sa.row_tiles = (G * t2 + 31) / 32;
+        sa.accum = t0 > 0;
+        if (D == 128) {
+            if (packed) MA_SCORE_I(128, SRC_PACKED);
+            else MA_SCORE_I(128, SRC_DENSE);
+        } else {
+            if (packed) MA_SCORE_I(64, SRC_PACKED);
+            else MA_SCORE_I(64, SRC_DENSE);
+        }
+        const int rc2 = ma_check_launch(who);
+        if (rc2) return rc2;
     }
 #undef MA_SCORE_I
 #undef MA_SCORE
-    return ma_check_launch(who);
+    return MA_OK;
 }

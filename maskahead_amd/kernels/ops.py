@@ -19,6 +19,7 @@ from .splitk import Prefix, prefix_scores, splitk_attention
 
 __all__ = [
     "KernelUnavailableError",
+    "_selected_queries",
     "SelectorResult",
     "SelectorScratch",
     "dense_packed_attention",
@@ -27,15 +28,22 @@ __all__ = [
     "quantize_values_into",
     "selector_topk",
     "hip_available",
+    "triton_available",
 ]
 
 
 def hip_available() -> bool:
+    """Whether the gfx950 kernels can run here: the library loads and a GPU is present."""
     try:
         N.load()
     except KernelUnavailableError:
         return False
     return torch.cuda.is_available()
+
+
+# the reference's name for "the GPU kernels can run" (ops.py:23-24); callers that probe
+# it before choosing a backend get the HIP answer
+triton_available = hip_available
 
 
 def _choose_backend(backend: str, tensor: torch.Tensor) -> str:
@@ -102,7 +110,7 @@ def _selected_queries(query: torch.Tensor, query_indices, hkv: int) -> torch.Ten
     b, hq, _, d = query.shape
     if hq % hkv:
         raise ValueError("Hq must be divisible by Hkv")
-    q = query[:, :, list(query_indices), :]
+    q = query[:, :, list(query_indices), :]          # [B, Hq, T2, D]; rows g * T2 + t2 per KV head
     return q.reshape(b, hkv, -1, d).contiguous()
 
 
@@ -153,6 +161,7 @@ def gather_packed_kv(view, indices, *, dtype=torch.bfloat16, backend="auto", out
     if idx.stride(-1) != 1:
         idx = idx.contiguous()
     prefix = Prefix.from_view(view)
+    prefix.check_mask(b, hkv)
     lib = N.load()
     rc = lib.ma_gather_kv(prefix.native(), b, hkv, d, idx.data_ptr(), N.i64arr(idx.stride(0), idx.stride(1)), k,
                           N.t4(out_key), N.t4(out_value), N.stream_of(idx))

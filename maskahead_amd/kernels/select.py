@@ -5,9 +5,10 @@ with three kernel launches per call; ties at the k-th value go to the smaller in
 the result is deterministic (torch.topk leaves that order unspecified).
 
 The kernels keep each row's histogram in a state block that must be zero before its
-first use and that every call leaves zero again.  One state buffer per device is kept here
-and grown (zero-filled) when a call has more rows.  Calls share it, so calls that overlap
-in time (on two streams at once) must pass their own ``state``.  The scratch workspace is
+first use and that every call leaves zero again.  One state buffer per (device, stream)
+is kept here and grown (zero-filled) when a call has more rows: calls on one stream are
+ordered, so they can share it, and a call on another stream (a selector side stream)
+gets its own.  A caller may pass its own ``state`` instead.  The scratch workspace is
 per call.
 """
 
@@ -21,12 +22,14 @@ _STATES: dict = {}
 
 
 def _state(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The zero-initialised select state of `device`, at least nbytes."""
-    st = _STATES.get(device.index)
+    """The zero-initialised select state of (`device`, its current stream), at least nbytes."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    st = _STATES.get(key)
     if st is None or st.numel() < nbytes:
-        # the old one goes back to the caching allocator, which reuses it in stream order
+        # allocated and zero-filled on the current stream; the old one goes back to the
+        # caching allocator, which reuses it in that stream's order
         st = torch.zeros((nbytes,), device=device, dtype=torch.uint8)
-        _STATES[device.index] = st
+        _STATES[key] = st
     return st
 
 

@@ -12,7 +12,8 @@ bf16 copy -- nibble unpack and scale/zero dequant happen in the load path of eve
 kernel -- and the split count is chosen for 256 CUs, not from the Triton tile sizes.
 The Triton tuning arguments (block_m, block_n, num_warps, fused_max) are accepted and
 ignored; dequant_rows / packed_direct_max still decide, as in the reference, whether
-the value distance reads V rounded to bf16 (the reference's unpacked copy) or in f32.
+the value distance reads V rounded to the query dtype (the reference's unpacked copy)
+or in f32.
 """
 
 from __future__ import annotations
@@ -25,8 +26,9 @@ from .. import _native as N
 class Prefix:
     """The prefix a kernel reads: packed (+ 16-bit residual tail) or plain 16-bit,
     [B, Hkv, n, D] (splitk.py:408-462).  ``mask``: optional uint8 [B, Hkv, n],
-    0 = dead slot.  ``vround``: set by splitk_attention when the reference would have
-    read this prefix through its bf16 unpacked copy."""
+    0 = dead slot.  ``vround``: 0, or the dtype code (MA_BF16 / MA_F16) of the unpacked
+    copy the reference would read this packed prefix through (splitk.py:513-516); only
+    the copy splitk_attention hands back in its statistics carries it."""
 
     __slots__ = ("kq", "ks", "kz", "vq", "vs", "vz", "kf", "vf", "nq", "nf", "kb", "vb", "kg", "vg", "mask",
                  "kmode", "kch", "vround")
@@ -38,7 +40,21 @@ class Prefix:
         self.kq, self.ks, self.kz, self.vq, self.vs, self.vz = kq, ks, kz, vq, vs, vz
         self.kf, self.vf, self.nq, self.nf = kf, vf, int(nq), int(nf)
         self.kb, self.vb, self.kg, self.vg = kb, vb, kg, vg
-        self.vround = False
+        self.vround = 0
+
+    def with_vround(self, code: int) -> "Prefix":
+        """A copy (same tensors) whose packed values are read rounded to dtype `code`."""
+        p = Prefix(kq=self.kq, ks=self.ks, kz=self.kz, vq=self.vq, vs=self.vs, vz=self.vz, kf=self.kf, vf=self.vf,
+                   nq=self.nq, nf=self.nf, kb=self.kb, vb=self.vb, kg=self.kg, vg=self.vg, mask=self.mask,
+                   kmode=self.kmode, kch=self.kch)
+        p.vround = int(code)
+        return p
+
+    def check_mask(self, b: int, hkv: int) -> None:
+        """The kernels index the mask as (b * Hkv + h) * n + j: it must be exactly [B, Hkv, n]."""
+        m = self.mask
+        if m is not None and tuple(m.shape) != (b, hkv, self.n):
+            raise ValueError(f"prefix mask must have shape {(b, hkv, self.n)}, got {tuple(m.shape)}")
 
     @property
     def n(self) -> int:
@@ -155,8 +171,12 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
     b, hq, t, d, hkv = _check_query(query, current_key)
     g = hq // hkv
     r = g * t
-    if prefix.nq and (r > dequant_rows or prefix.n > packed_direct_max):
-        prefix.vround = True         # the reference reads its bf16 unpacked copy from here on
+    prefix.check_mask(b, hkv)
+    # the reference unpacks such a prefix to query.dtype and reads that copy from here on
+    # (splitk.py:513-516); the statistics carry a copy that says so
+    used = prefix
+    if prefix.nq and (r > dequant_rows or prefix.n > packed_direct_max) and query.dtype != torch.float32:
+        used = prefix.with_vround(N.dtype_code(query.dtype))
     dev = query.device
     scale = float(scaling) if scaling is not None else d ** -0.5
     out = torch.empty_like(query)
@@ -179,7 +199,7 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
         N.t4(out), N.ptr(mp), N.ptr(lp), N.ptr(op), int(split_tokens), ws.data_ptr(), ws_bytes,
         N.stream_of(query))
     N.check(rc, "ma_splitk_attention")
-    return out, ((mp, lp, op, prefix) if want_prefix else None)
+    return out, ((mp, lp, op, used) if want_prefix else None)
 
 
 def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: bool, scaling=None,
@@ -194,6 +214,7 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
     hkv = mp.shape[1]
     g = hq // hkv
     n = prefix.n
+    prefix.check_mask(b, hkv)
     if not q_rows.is_cuda and q_rows.numel() and (int(q_rows.min()) < 0 or int(q_rows.max()) >= t):
         raise ValueError(f"q_rows must be block positions in [0, {t})")
     q_rows = q_rows.to(device=query.device, dtype=torch.int32).contiguous()   # device rows: clamped in-kernel
@@ -209,7 +230,7 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
     if value and (not op.is_contiguous() or tuple(op.shape) != (b, hkv, g * t, d)):
         raise ValueError("stats O_p must be a contiguous [B, Hkv, R, D] tensor")
     scale = float(scaling) if scaling is not None else d ** -0.5
-    vround = 1 if (prefix.nq and prefix.vround) else 0
+    vround = int(prefix.vround) if prefix.nq else 0
     rc = lib.ma_prefix_scores(N.t4(query), b, hq, t, d, prefix.native(), hkv, q_rows.data_ptr(), t2,
                               mp.data_ptr(), lp.data_ptr(), op.data_ptr() if value else None,
                               N.dtype_code(op.dtype) if value else 0, scale, 1 if value else 0, vround,

@@ -105,11 +105,14 @@ class FastLayerPath:
     value_aware: bool = True
     sort_indices: bool = True
     compute_dtype: torch.dtype = torch.bfloat16
+    dense_prefix_layers: int = 0
+    semantic: str = "A"
     slot_masks: dict = field(default_factory=dict)
     states: dict = field(default_factory=dict)
     last_mass: dict = field(default_factory=dict)
     probe_mass: dict = field(default_factory=dict)
     chunk_mass: dict = field(default_factory=dict)
+    qprobe_mass: dict = field(default_factory=dict)
     _rows_cache: tuple | None = None
 
     @property
@@ -198,11 +201,13 @@ class FastLayerPath:
         return state
 
     def step0(self, layer_idx, query, current_key, current_value, *, select: bool, topk: int,
-              want_mass: bool = False):
+              want_mass: bool = False, live_slots=None):
         """Step 0 of a block (session.py:1403-1454): attention over the live prefix and,
         when `select`, the block's read set of `topk` entries per KV head ranked by mass
         (or mass * ||v - c|| when value_aware), gathered into the compact buffer.  The
-        prefix mass is kept in last_mass[layer_idx] when want_mass (eviction input)."""
+        prefix mass is kept in last_mass[layer_idx] when want_mass (eviction input): per
+        physical slot, or in live order when live_slots [B, Hkv, live] (the eviction state's
+        slots of this layer) is given, as the reference's _to_live (session.py:257-261)."""
         need_sel = select and bool(self.query_indices)
         need_mass = want_mass and bool(self.query_indices)
         prefix = self.prefix(layer_idx)
@@ -217,7 +222,7 @@ class FastLayerPath:
         value = need_sel and self.value_aware
         mass, score = prefix_scores(query, prefix, stats, rows, value=value, scaling=scale)
         if need_mass:
-            self.last_mass[layer_idx] = mass
+            self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
         if need_sel:
             k = min(int(topk), prefix.n)
             if k <= 0:
@@ -250,3 +255,73 @@ class FastLayerPath:
         out, _ = splitk_attention(query.to(cd), pre, current_key.to(cd), current_value.to(cd),
                                   scaling=self.head_dim ** -0.5)
         return out.to(query.dtype)
+
+    def question_probe(self, layer_idx, query, current_key, current_value, *, q_pos0: int, live_slots=None):
+        """A question-probe forward (session.py:2289-2297): block-causal attention from block
+        position q_pos0 over [live prefix | probe tokens]; the prefix mass of every probe
+        query goes to qprobe_mass[layer_idx] (live order when live_slots is given)."""
+        t = query.shape[2]
+        out, mass = self.attend(layer_idx, query, current_key, current_value, causal=self.block_size,
+                                q_pos0=q_pos0, mass_rows=list(range(t)))
+        if mass is not None:
+            self.qprobe_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
+        return out
+
+    def dense_required(self, layer_idx: int, ctx: "BlockContext") -> bool:
+        """Whether this layer attends the whole live prefix instead of a read set
+        (session.py:456-467)."""
+        if self.semantic == "dense" or layer_idx < self.dense_prefix_layers:
+            return True
+        if ctx.evicting:
+            return ctx.live_len == 0 or not self.query_indices
+        return ctx.old_cache_len == 0 or ctx.topk >= ctx.old_cache_len or not self.query_indices
+
+    def route(self, layer_idx, query, current_key, current_value, ctx: "BlockContext"):
+        """One layer's attention call on the fast path, sent where the reference session's
+        attend hook sends it (_attend_entry / _attend_main, session.py:2281-2418): a prefill
+        chunk, a question probe, a lookahead probe, step 0 of a block (dense layers: the
+        attention, and the mass when wanted; sparse layers: also the read set), or a later
+        denoising sub-step (dense layers: over the live prefix; sparse layers: over the
+        read set)."""
+        live = None if ctx.live_slots is None else ctx.live_slots.get(layer_idx)
+        if ctx.prefill:
+            return self.prefill_chunk(layer_idx, query, current_key, current_value, want_mass=ctx.want_mass,
+                                      live_slots=live)
+        if ctx.qprobe_start is not None:
+            return self.question_probe(layer_idx, query, current_key, current_value, q_pos0=ctx.qprobe_start,
+                                       live_slots=live)
+        if ctx.probe:
+            return self.probe(layer_idx, query, current_key, current_value, live_slots=live)
+        dense = self.dense_required(layer_idx, ctx)
+        if ctx.step_index == 0:
+            return self.step0(layer_idx, query, current_key, current_value,
+                              select=not dense and self.semantic == "A", topk=ctx.topk, want_mass=ctx.want_mass,
+                              live_slots=live)
+        if dense:
+            return self.attend(layer_idx, query, current_key, current_value)[0]
+        return self.compact_attention(layer_idx, query, current_key, current_value)
+
+
+@dataclass
+class BlockContext:
+    """The session state one layer call is routed on (the reference session's fields).
+
+    step_index: denoising step within the block (0 = the step that selects);
+    probe: a lookahead probe forward (session._probe); prefill: a prefill-chunk forward
+    (session._prefill_mode); qprobe_start: block position of a question probe, or None;
+    old_cache_len: prefix length when the block began; topk: the block's read budget
+    (config.effective_topk); evicting: eviction is on, so the cache is the live set;
+    live_len: live entries per lane; want_mass: step 0 / the chunk keeps its prefix mass
+    (lookahead pending, EMA policies); live_slots: per layer, the eviction state's slots
+    [B, Hkv, live] that put masses in live order (None: per physical slot)."""
+
+    step_index: int = 0
+    probe: bool = False
+    prefill: bool = False
+    qprobe_start: int | None = None
+    old_cache_len: int = 0
+    topk: int = 0
+    evicting: bool = False
+    live_len: int = 0
+    want_mass: bool = False
+    live_slots: dict | None = None

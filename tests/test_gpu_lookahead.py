@@ -101,3 +101,39 @@ def test_lookahead_probe_evict_then_masked_attention(gpu):
         gi = new_phys[layer].unsqueeze(-1).expand(-1, -1, -1, d)
         want = OA.dense_attention(q3, kd2[layer].gather(2, gi), vd2[layer].gather(2, gi), k3, v3)
         assert_attention_close(out, want)
+
+    # a second cycle over the rebuilt cache, where the slots of the live entries are no
+    # longer 0..live-1: step 0 and the probe hand back their masses in live order, the
+    # lookahead score and the keep set follow from them
+    live = st.live
+    assert not torch.equal(new_phys[0], torch.arange(live).expand_as(new_phys[0]))
+    a1b = {}
+    qp2 = torch.randn((1, hq, 2 * t, d), generator=g).to(torch.bfloat16)
+    kp2 = torch.randn((1, hkv, 2 * t, d), generator=g).to(torch.bfloat16)
+    vp2 = torch.randn((1, hkv, 2 * t, d), generator=g).to(torch.bfloat16)
+    for layer in range(L):
+        slots = st.phys[layer, ..., :live]
+        mask = fp.slot_masks[layer].cpu()
+        fp.step0(layer, q3.to(gpu), k3.to(gpu), v3.to(gpu), select=False, topk=1, want_mass=True, live_slots=slots)
+        a1b[layer] = fp.last_mass[layer]
+        assert a1b[layer].shape == (1, hkv, live)
+        _, mp, lp, _ = OA.splitk_attention(q3, kd2[layer], vd2[layer], k3, v3, mask=mask)
+        wmass, _ = OA.prefix_scores(q3, kd2[layer], None, mp, lp, None, list(range(t)), mask=mask,
+                                    value_aware=False)
+        assert rel_err(a1b[layer], wmass.gather(-1, new_phys[layer])) < 2e-3
+        fp.probe(layer, qp2.to(gpu), kp2.to(gpu), vp2.to(gpu), live_slots=slots)
+        _, mpp, lpp, _ = OA.splitk_attention(qp2, kd2[layer], vd2[layer], kp2, vp2, causal_block=t, mask=mask)
+        wpm, _ = OA.prefix_scores(qp2, kd2[layer], None, mpp, lpp, None, list(range(t, 2 * t)), mask=mask,
+                                  value_aware=False)
+        assert rel_err(fp.probe_mass[layer], wpm.gather(-1, new_phys[layer])) < 2e-3
+    score2 = lookahead_scores(cache, st, a1b, fp.probe_mass, use_value=True)
+    for layer in range(L):
+        a = (a1b[layer] + fp.probe_mass[layer]).cpu()
+        gi = new_phys[layer].unsqueeze(-1).expand(-1, -1, -1, d)
+        assert torch.equal(score2[layer].cpu(), OA.value_score_bf16(a, vd2[layer].gather(2, gi)))
+    C2 = 768
+    pos1 = st.pos[..., :live].cpu().to(torch.int64)
+    keep2 = lookahead_evict(cache, st, cfg, C2, a1b, fp.probe_mass, next_position=n)
+    torch.cuda.synchronize()
+    assert torch.equal(keep2.cpu(), OS.keep_select(pos1, score2.cpu(), C2, W))
+    assert st.live == C2

@@ -106,3 +106,25 @@ def test_value_score_fp32_vs_bf16_branch():
     s16 = OA.value_score_bf16(a, v)
     s32 = OA.value_score_fp32(a, v)
     assert torch.allclose(s16, s32, rtol=2e-2)
+
+
+def test_dense_attention_matches_sdpa_and_brute_force():
+    """oracle.dense_attention (reference.py:279-315, the sub-step's sdpa_compact) against
+    torch's SDPA with the KV heads repeated per GQA group, and against an explicit
+    per-(head, query) softmax loop on a tiny case."""
+    q, k, v, kc, vc = layer_inputs(hq=12, hkv=3, d=32, n=50, t=6, seed=17, dtype=F64)
+    got = OA.dense_attention(q, k, v, kc, vc)
+    want = _sdpa(q, torch.cat([k, kc], 2), torch.cat([v, vc], 2))
+    assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+    # brute force: head h reads KV head h // 4; one softmax per query row
+    kk, vv = torch.cat([k, kc], 2), torch.cat([v, vc], 2)
+    for h in (0, 5, 11):
+        for t in (0, 5):
+            s = torch.tensor([float((q[0, h, t] * kk[0, h // 4, j]).sum()) / math.sqrt(32) for j in range(56)],
+                             dtype=F64)
+            w = torch.exp(s - s.max())
+            o = (w[:, None] * vv[0, h // 4]).sum(0) / w.sum()
+            assert torch.allclose(got[0, h, t], o, rtol=1e-12, atol=1e-12)
+    # a custom scale enters the logits only
+    half = OA.dense_attention(q, k, v, kc, vc, scale=0.5 / math.sqrt(32))
+    assert torch.allclose(half, OA.dense_attention(q * 0.5, k, v, kc, vc), rtol=1e-12, atol=1e-12)
