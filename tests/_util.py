@@ -108,3 +108,55 @@ def same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
     if a.element_size() == 2 and a.is_floating_point():
         a, b = a.view(torch.int16), b.view(torch.int16)
     return torch.equal(a, b)
+
+
+def check_read_set(tag: str, idx, gpu_score, same_stats_score, e2e_score, k: int, mask=None) -> dict:
+    """Read-set parity of a step 0, with its tolerance band derived from measured errors.
+
+    idx: the GPU's read set [..., k]; gpu_score: the GPU's scores; same_stats_score: the
+    oracle's scores computed from the GPU's own prefix statistics (M_p, L_p, O_p) -- so
+    the two differ only by the f32 reduction order of the score pass; e2e_score: the
+    oracle's scores from its own float64 statistics.  Against each oracle set, every
+    member that differs must lie within 2 * (measured relative score error) + 1e-6 of
+    the k-th oracle score.  The counts are returned, and appended as one JSON line to
+    the file $MASKAHEAD_PARITY_RECORD when that is set."""
+    import json
+    import os
+
+    from oracle import selection as OS
+
+    out = {"case": tag, "k": k}
+    for name, ref in (("same_stats", same_stats_score), ("end_to_end", e2e_score)):
+        err = rel_err(gpu_score if mask is None else gpu_score * mask.to(gpu_score.device),
+                      ref if mask is None else ref * mask)
+        band = 2 * err + 1e-6
+        ok, nmis, worst = OS.boundary_mismatch_ok(idx, OS.topk_ascending(ref, k, mask), ref, k, rel=band, mask=mask)
+        out[name] = {"score_rel_err": float(err), "band": float(band), "mismatches": int(nmis),
+                     "worst_boundary_rel": float(worst), "ok": bool(ok)}
+    rec = os.environ.get("MASKAHEAD_PARITY_RECORD")
+    if rec:
+        with open(rec, "a") as f:
+            f.write(json.dumps(out) + "\n")
+    print(out)
+    assert out["same_stats"]["ok"] and out["end_to_end"]["ok"], out
+    return out
+
+
+def fastpath_read_set(tag, fp, layer, q, kc, vc, kd, vd, rows, k, e2e_stats, mask=None, heads=None) -> dict:
+    """check_read_set for a FastLayerPath step 0 of `layer` (GPU tensors q, kc, vc; CPU
+    oracle view kd, vd of the layer): the GPU's scores and statistics are recomputed by the
+    same deterministic passes step 0 ran; e2e_stats = the oracle's (M_p, L_p, O_p).
+    heads: optional slice of KV heads to check (the oracle's view and stats cover them)."""
+    from maskahead_amd.kernels.splitk import prefix_scores, splitk_attention
+
+    hs = heads if heads is not None else slice(None)
+    pre = fp.prefix(layer)
+    _, st = splitk_attention(q, pre, kc, vc, want_prefix=True)
+    _, gscore = prefix_scores(q, pre, st, torch.as_tensor(list(rows), dtype=torch.int32), value=True)
+    gmp, glp, gop = (x[:, hs].cpu() for x in st[:3])
+    g = q.shape[1] // kc.shape[1]
+    qh = q.cpu() if heads is None else q[:, hs.start * g:hs.stop * g].cpu()
+    m = None if mask is None else mask[:, hs].cpu()
+    _, sscore = OA.prefix_scores(qh, kd, vd.float(), gmp, glp, gop, list(rows), mask=m, value_aware=True)
+    _, wscore = OA.prefix_scores(qh, kd, vd.float(), *e2e_stats, list(rows), mask=m, value_aware=True)
+    return check_read_set(tag, fp.states[layer].indices[:, hs].cpu(), gscore[:, hs].cpu(), sscore, wscore, k, mask=m)

@@ -16,7 +16,7 @@ from maskahead_amd.workloads import CONFIGS, layer_inputs
 from oracle import attention as OA
 from oracle import selection as OS
 
-from _util import assert_attention_close, rel_err
+from _util import assert_attention_close, fastpath_read_set, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -129,11 +129,10 @@ def test_fastpath_step0_substeps_probe(gpu, packed, t):
     out = fp.step0(0, qg, kcg, vcg, select=True, topk=k_read)
     wout, wmp, wlp, wop = OA.splitk_attention(qb, kd, vd, kcb, vcb)
     assert_attention_close(out, wout)
-    _, wscore = OA.prefix_scores(qb, kd, vd.float(), wmp, wlp, wop, list(range(t)), value_aware=True)
+    fastpath_read_set(f"fastpath_step0_{'k4v4' if packed else 'bf16'}_t{t}", fp, 0, qg, kcg, vcg, kd, vd,
+                      range(t), k_read, (wmp, wlp, wop))
     st = fp.states[0]
     idx = st.indices.cpu()
-    ok, nmis, worst = OS.boundary_mismatch_ok(idx, OS.topk_ascending(wscore, k_read), wscore, k_read, rel=2e-3)
-    assert ok, (nmis, worst)
     gi = idx.unsqueeze(-1).expand(-1, -1, -1, d)
     assert torch.equal(st.key[:, :, :k_read].cpu(), kd.gather(2, gi))
     assert torch.equal(st.value[:, :, :k_read].cpu(), vd.gather(2, gi))
@@ -155,7 +154,7 @@ def test_fastpath_step0_substeps_probe(gpu, packed, t):
     wout_p, wmp_p, wlp_p, _ = OA.splitk_attention(qb, kd, vd, kcb, vcb, causal_block=8, q_pos0=n, c_pos0=n)
     assert_attention_close(out_p, wout_p)
     wmass, _ = OA.prefix_scores(qb, kd, None, wmp_p, wlp_p, None, rows, value_aware=False)
-    assert rel_err(mass, wmass) < 2e-3
+    assert rel_err(mass, wmass) < 1e-4
 
 
 def test_config3_keep_step(gpu):
@@ -176,7 +175,7 @@ def test_config3_keep_step(gpu):
                                             q_pos0=sh.n, c_pos0=sh.n)
     assert_attention_close(out[:, :8], wout)
     wmass, _ = OA.prefix_scores(q[:, :8], k[:, hs], None, wmp, wlp, None, range(sh.t), value_aware=False)
-    assert rel_err(mass[:, hs], wmass) < 2e-3
+    assert rel_err(mass[:, hs], wmass) < 1e-4
     assert torch.all(mass >= 0)
     # keep score and keep set on the GPU's own mass: bit-exact against the oracle
     view = cache.layer_view(0)
@@ -222,14 +221,13 @@ def test_config4_ragged_batch_step0_and_keep(gpu):
         out = fp.step0(layer, qb.to(gpu), kcb.to(gpu), vcb.to(gpu), select=True, topk=k_read, want_mass=True)
         wout, wmp, wlp, wop = OA.splitk_attention(qb, kd, vd, kcb, vcb, mask=mask)
         assert_attention_close(out, wout)
-        wmass, wscore = OA.prefix_scores(qb, kd, vd.float(), wmp, wlp, wop, list(range(t)), mask=mask,
-                                         value_aware=True)
-        assert rel_err(fp.last_mass[layer].cpu() + (1 - mask), wmass + (1 - mask)) < 2e-3
+        wmass, _ = OA.prefix_scores(qb, kd, vd.float(), wmp, wlp, wop, list(range(t)), mask=mask,
+                                    value_aware=True)
+        assert rel_err(fp.last_mass[layer].cpu() + (1 - mask), wmass + (1 - mask)) < 1e-4
+        fastpath_read_set(f"ragged_batch_layer{layer}", fp, layer, qb.to(gpu), kcb.to(gpu), vcb.to(gpu), kd, vd,
+                          range(t), k_read, (wmp, wlp, wop), mask=mask)
         st = fp.states[layer]
         idx = st.indices.cpu()
-        ok, nmis, worst = OS.boundary_mismatch_ok(idx, OS.topk_ascending(wscore, k_read, mask), wscore, k_read,
-                                                  rel=2e-3, mask=mask)
-        assert ok, (layer, nmis, worst)
         assert bool(torch.all(mask.gather(2, idx) == 1))          # only live slots are read
         gi = idx.unsqueeze(-1).expand(-1, -1, -1, d)
         assert torch.equal(st.key[:, :, :k_read].cpu(), kd.gather(2, gi))

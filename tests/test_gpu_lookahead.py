@@ -58,13 +58,13 @@ def test_lookahead_probe_evict_then_masked_attention(gpu):
         a1[layer] = fp.last_mass[layer]
         _, mp, lp, _ = OA.splitk_attention(qb, kd, vd, kcb, vcb)
         wmass, _ = OA.prefix_scores(qb, kd, None, mp, lp, None, list(range(t)), value_aware=False)
-        assert rel_err(a1[layer], wmass) < 2e-3
+        assert rel_err(a1[layer], wmass) < 1e-4
         # probe of blocks k+1 .. k+3: block-causal, the mass of blocks k+2, k+3 counted per block
         out_p = fp.probe(layer, qp.to(gpu), kp.to(gpu), vp.to(gpu), live_slots=st.phys[layer, ..., :st.live])
         wout_p, mpp, lpp, _ = OA.splitk_attention(qp, kd, vd, kp, vp, causal_block=t, q_pos0=0, c_pos0=0)
         assert_attention_close(out_p, wout_p)
         wpm, _ = OA.prefix_scores(qp, kd, None, mpp, lpp, None, list(range(t, 3 * t)), value_aware=False)
-        assert rel_err(fp.probe_mass[layer], wpm * 2) < 2e-3
+        assert rel_err(fp.probe_mass[layer], wpm * 2) < 1e-4
 
     # the lookahead score from the GPU masses: value_score in bf16, bit-exact
     score = lookahead_scores(cache, st, a1, fp.probe_mass, use_value=True)
@@ -120,12 +120,12 @@ def test_lookahead_probe_evict_then_masked_attention(gpu):
         _, mp, lp, _ = OA.splitk_attention(q3, kd2[layer], vd2[layer], k3, v3, mask=mask)
         wmass, _ = OA.prefix_scores(q3, kd2[layer], None, mp, lp, None, list(range(t)), mask=mask,
                                     value_aware=False)
-        assert rel_err(a1b[layer], wmass.gather(-1, new_phys[layer])) < 2e-3
+        assert rel_err(a1b[layer], wmass.gather(-1, new_phys[layer])) < 1e-4
         fp.probe(layer, qp2.to(gpu), kp2.to(gpu), vp2.to(gpu), live_slots=slots)
         _, mpp, lpp, _ = OA.splitk_attention(qp2, kd2[layer], vd2[layer], kp2, vp2, causal_block=t, mask=mask)
         wpm, _ = OA.prefix_scores(qp2, kd2[layer], None, mpp, lpp, None, list(range(t, 2 * t)), mask=mask,
                                   value_aware=False)
-        assert rel_err(fp.probe_mass[layer], wpm.gather(-1, new_phys[layer])) < 2e-3
+        assert rel_err(fp.probe_mass[layer], wpm.gather(-1, new_phys[layer])) < 1e-4
     score2 = lookahead_scores(cache, st, a1b, fp.probe_mass, use_value=True)
     for layer in range(L):
         a = (a1b[layer] + fp.probe_mass[layer]).cpu()
