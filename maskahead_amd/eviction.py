@@ -2,9 +2,9 @@
 
 Drop-in for the reference's ``maskahead.eviction`` on the paths the GPU keep step uses
 (eviction.py:55-457).  ``EvictionConfig`` keeps the reference's field names, defaults and
-validation so the same YAML files load; ``EvictionState`` keeps its arrays (g, n, pos,
-phys per (layer, batch, KV head) lane, live axis last) on the GPU, and its two hot
-operations run in gfx950 kernels:
+validation so the same YAML files load (an interface); ``EvictionState`` is a column
+store of the live entries of every (layer, batch, KV head) lane on the GPU, and its two
+hot operations run in gfx950 kernels:
 
     keep = state.survivors(cfg, capacity, spread, score)   # ma_keep_select
     state.compact(keep)                                    # ma_compact_tokens, in place
@@ -28,6 +28,7 @@ Policy = Literal["none", "recent", "ema_recent", "ema_recent_value", "ema_recent
 _POLICIES = ("none", "recent", "ema_recent", "ema_recent_value", "ema_recent_score", "expected_attention",
              "greedy_set", "oracle_future", "lookahead", "snapkv")
 _SCORED = ("expected_attention", "greedy_set", "oracle_future", "lookahead")
+_EMA_POLICIES = ("ema_recent", "ema_recent_value", "ema_recent_score")
 
 
 @dataclass(slots=True)
@@ -111,162 +112,180 @@ class EvictionConfig:
 
 
 class EvictionState:
-    """Per (layer, batch, KV head) live-entry state (eviction.py:205-457): g f32, n int16,
-    pos int32 (int64 when max_position >= 2^31), phys int32, shape [L, B, Hkv, capacity],
-    the first ``live`` slots in use and ordered by position."""
+    """The live set of every (layer, batch, KV head) lane, as columns on the GPU.
+
+    Four columns, each [L, B, Hkv, rows] with the live axis last and the first ``live``
+    rows in use, ordered by position (the reference's EvictionState arrays,
+    eviction.py:205-281): ``g`` f32 attention EMA, ``n`` int16 observation count, ``pos``
+    token position (int32, int64 when max_position >= 2^31), ``phys`` the entry's physical
+    slot in the cache.  Every lane of a state holds the same number of live entries.
+
+    Keep-set selection reduces every policy to one contest -- a recency window kept
+    outright plus the top of a per-entry rank among the rest, sinks and pinned positions
+    ranking +inf -- solved for all lanes in one ma_keep_select call; compaction moves the
+    four columns in one ma_compact_tokens call."""
+
+    _COLUMNS = ("g", "n", "pos", "phys")
 
     def __init__(self, *, num_layers: int, batch_size: int, num_kv_heads: int, capacity: int,
                  device: torch.device | str, max_position: int = 1 << 31) -> None:
-        self.num_layers = int(num_layers)
-        self.batch_size = int(batch_size)
-        self.num_kv_heads = int(num_kv_heads)
+        self.num_layers, self.batch_size, self.num_kv_heads = int(num_layers), int(batch_size), int(num_kv_heads)
         self.device = torch.device(device)
         self.pos_dtype = torch.int32 if max_position < (1 << 31) else torch.int64
-        shape = (self.num_layers, self.batch_size, self.num_kv_heads, capacity)
-        self.g = torch.zeros(shape, dtype=torch.float32, device=self.device)
-        self.n = torch.zeros(shape, dtype=torch.int16, device=self.device)
-        self.pos = torch.zeros(shape, dtype=self.pos_dtype, device=self.device)
-        self.phys = torch.zeros(shape, dtype=torch.int32, device=self.device)
+        self._dtypes = {"g": torch.float32, "n": torch.int16, "pos": self.pos_dtype, "phys": torch.int32}
+        self._cols: dict[str, torch.Tensor] = {}
         self.live = 0
-        self._capacity = capacity
         self.pin: tuple[int | torch.Tensor, int] | None = None
+        self._ensure(max(int(capacity), 1))
 
-    # -- growth ------------------------------------------------------------
-    def _grow_to(self, needed: int) -> None:
-        if needed <= self._capacity:
+    # the columns, as attributes (views of the whole storage; rows >= live are unused)
+    g = property(lambda self: self._cols["g"])
+    n = property(lambda self: self._cols["n"])
+    pos = property(lambda self: self._cols["pos"])
+    phys = property(lambda self: self._cols["phys"])
+
+    @property
+    def rows(self) -> int:
+        return int(self._cols["pos"].shape[-1])
+
+    def _ensure(self, rows: int) -> None:
+        """At least `rows` rows per lane (doubling), live rows kept, new rows zero."""
+        have = self.rows if self._cols else 0
+        if rows <= have:
             return
-        new_cap = max(needed, self._capacity * 2, 1)
-        pad = new_cap - self._capacity
-        shape = (self.num_layers, self.batch_size, self.num_kv_heads, pad)
+        rows = max(rows, 2 * have)
+        lead = (self.num_layers, self.batch_size, self.num_kv_heads)
+        for name in self._COLUMNS:
+            col = torch.zeros(lead + (rows,), dtype=self._dtypes[name], device=self.device)
+            if self.live:
+                col[..., :self.live] = self._cols[name][..., :self.live]
+            self._cols[name] = col
 
-        def grow(t):
-            return torch.cat([t, torch.zeros(shape, dtype=t.dtype, device=self.device)], -1)
+    def _in_use(self, name: str, layer: int | None = None) -> torch.Tensor:
+        col = self._cols[name]
+        return col[..., :self.live] if layer is None else col[layer, ..., :self.live]
 
-        self.g, self.n, self.pos, self.phys = grow(self.g), grow(self.n), grow(self.pos), grow(self.phys)
-        self._capacity = new_cap
-
+    # -- admission and observation -------------------------------------------------------------
     def append(self, positions, phys: torch.Tensor | None = None) -> None:
-        """Admit new entries with g = 0, n = 0 (eviction.py:258-281)."""
-        if isinstance(positions, range):
-            positions = list(positions)
-        if isinstance(positions, list):
-            positions = torch.tensor(positions, dtype=self.pos_dtype, device=self.device)
-        m = int(positions.numel())
+        """Admit entries at `positions` (the same in every lane, increasing, after every
+        live position): EMA 0, never observed, slot = `phys` or the position."""
+        p = torch.as_tensor(list(positions) if isinstance(positions, range) else positions, device=self.device)
+        m = int(p.numel())
         if m == 0:
             return
-        self._grow_to(self.live + m)
-        sl = slice(self.live, self.live + m)
-        self.g[..., sl] = 0.0
-        self.n[..., sl] = 0
-        self.pos[..., sl] = positions.to(self.pos_dtype).view(1, 1, 1, m)
-        self.phys[..., sl] = (positions if phys is None else phys).to(self.phys.dtype).view(1, 1, 1, m)
+        self._ensure(self.live + m)
+        rows = slice(self.live, self.live + m)
+        fill = {"g": 0, "n": 0, "pos": p.view(1, 1, 1, m), "phys": (p if phys is None else phys).view(1, 1, 1, m)}
+        for name, value in fill.items():
+            self._cols[name][..., rows] = value
         self.live += m
 
-    # -- update ------------------------------------------------------------
     def observe(self, layer_idx: int, alpha: torch.Tensor, decay: float, weight: float = 1.0) -> None:
-        """Fold a block's attention mass into the EMA of one layer (eviction.py:284-308)."""
+        """Fold one block's attention mass alpha [B, Hkv, live] of layer `layer_idx` into its
+        EMA: g <- decay * g + (1 - decay) * alpha, or g <- g + weight * alpha when decay is
+        1 (H2O's accumulated attention over `weight` queries); n counts the observations.
+        The torch operations are the reference's (eviction.py:284-308, scale then add the
+        weighted mass), so that g has the same bits."""
         if self.live == 0:
             return
         if alpha.shape[-1] != self.live:
             raise ValueError(f"alpha has {alpha.shape[-1]} entries but {self.live} are live; "
                              "the selector must rank exactly the live set")
-        sl = slice(0, self.live)
-        g = self.g[layer_idx, ..., sl]
+        g = self._in_use("g", layer_idx)
+        a = alpha.to(torch.float32)
         if decay == 1.0:
-            g.add_(alpha.to(g.dtype), alpha=float(weight))
+            g.add_(a, alpha=float(weight))
         else:
-            g.mul_(decay).add_(alpha.to(g.dtype), alpha=1.0 - decay)
-        self.n[layer_idx, ..., sl] += 1
+            g.mul_(decay).add_(a, alpha=1.0 - decay)
+        self._in_use("n", layer_idx).add_(1)
 
     def corrected(self, layer_idx: int, decay: float) -> torch.Tensor:
-        """ghat = g / (1 - decay**n), 0 where n == 0 (eviction.py:310-322)."""
-        sl = slice(0, self.live)
-        g = self.g[layer_idx, ..., sl]
-        n = self.n[layer_idx, ..., sl]
+        """The bias-corrected EMA g / (1 - decay^n) of one layer, 0 where never observed
+        (eviction.py:310-322); g itself when decay is 0 or 1."""
+        g, n = self._in_use("g", layer_idx), self._in_use("n", layer_idx)
         if decay in (0.0, 1.0):
             return g.clone()
-        denom = 1.0 - torch.pow(torch.tensor(decay, dtype=torch.float32, device=g.device), n.to(torch.float32))
-        return torch.where(n > 0, g / denom.clamp_min(1e-8), torch.zeros_like(g))
+        seen = n > 0
+        scale = 1.0 - torch.pow(torch.tensor(decay, dtype=torch.float32, device=g.device), n.to(torch.float32))
+        return torch.where(seen, g / scale.clamp_min(1e-8), torch.zeros_like(g))
 
-    # -- eviction ----------------------------------------------------------
+    # -- keep-set selection ----------------------------------------------------------------------
+    def _contest(self, cfg: EvictionConfig, capacity: int, value_spread, score) -> tuple[torch.Tensor, int]:
+        """(rank [L, B, Hkv, live] f32, window) of a policy (eviction.py:325-409): the window's
+        newest entries are kept outright, the rest of the budget goes to the highest rank."""
+        live_shape = (self.num_layers, self.batch_size, self.num_kv_heads, self.live)
+        policy = cfg.policy
+        if policy == "recent":                        # StreamingLLM: the newest (+ sinks, pins)
+            return self._in_use("pos").to(torch.float32), 0
+        if policy == "snapkv":                        # its observation window + pooled attention
+            if score is None or tuple(score.shape) != live_shape:
+                raise ValueError("policy snapkv needs a [L, B, Hkv, live] score")
+            return score.to(torch.float32), cfg.snapkv_window
+        if policy not in _EMA_POLICIES + _SCORED:
+            raise ValueError(f"policy {policy} does not evict")
+        window = min(cfg.recent_window, capacity)
+        if capacity == window:                        # the window is the whole budget
+            return torch.zeros(live_shape, dtype=torch.float32, device=self.device), window
+        if policy in _SCORED:
+            if score is None or tuple(score.shape) != live_shape:
+                raise ValueError(f"policy {policy} needs a [L, B, Hkv, live] score")
+            return score.to(torch.float32), window
+        rank = torch.stack([self.corrected(layer, cfg.decay) for layer in range(self.num_layers)])
+        if policy == "ema_recent_value":
+            if value_spread is None:
+                raise ValueError("policy ema_recent_value needs value_spread; the caller must supply "
+                                 "per-entry ||v - vbar||")
+            if tuple(value_spread.shape) != live_shape:
+                raise ValueError(f"value_spread has shape {tuple(value_spread.shape)} but the live EMA "
+                                 f"is {live_shape}")
+            if cfg.value_caote:
+                share = rank / rank.sum(dim=-1, keepdim=True).clamp_min(1e-12)
+                rank = share / (1.0 - share).clamp_min(1e-6)
+            rank = rank * value_spread.to(rank.dtype)
+        return rank, window
+
     def survivors(self, cfg: EvictionConfig, capacity: int, value_spread: torch.Tensor | None = None,
                   score: torch.Tensor | None = None) -> torch.Tensor:
-        """Live-axis indices to keep, [L, B, Hkv, capacity], in position order
-        (eviction.py:325-409).  Every policy reduces to one ma_keep_select launch over
-        all lanes: a recency window that is always kept, plus the top of a rank among
-        the rest where sinks and pinned positions rank +inf."""
-        sl = slice(0, self.live)
-        pos = self.pos[..., sl]
-        if cfg.policy == "recent":
-            # the C newest, sinks and pins first: rank by position, window 0
-            rank = pos.to(torch.float32)
-            return keep_select(pos, rank, capacity, 0, sink_tokens=cfg.sink_tokens, pin=self._pin_rows())
-        if cfg.policy == "snapkv":
-            if score is None or score.shape != self.g.shape[:3] + (self.live,):
-                raise ValueError("policy snapkv needs a [L, B, Hkv, live] score")
-            return keep_select(pos, score.to(torch.float32), capacity, cfg.snapkv_window,
-                               sink_tokens=cfg.sink_tokens, pin=self._pin_rows())
-        if cfg.policy in ("ema_recent", "ema_recent_value", "ema_recent_score") + _SCORED:
-            w = min(cfg.recent_window, capacity)
-            if capacity - w > 0:
-                ghat = torch.stack([self.corrected(l, cfg.decay) for l in range(self.num_layers)], dim=0)
-                if cfg.policy in _SCORED:
-                    if score is None or score.shape != ghat.shape:
-                        raise ValueError(f"policy {cfg.policy} needs a [L, B, Hkv, live] score")
-                    ghat = score.to(ghat.dtype)
-                if cfg.policy == "ema_recent_value":
-                    if value_spread is None:
-                        raise ValueError("policy ema_recent_value needs value_spread; the caller must supply "
-                                         "per-entry ||v - vbar||")
-                    if value_spread.shape != ghat.shape:
-                        raise ValueError(f"value_spread has shape {tuple(value_spread.shape)} but the live EMA "
-                                         f"is {tuple(ghat.shape)}")
-                    if cfg.value_caote:
-                        norm = ghat / ghat.sum(dim=-1, keepdim=True).clamp_min(1e-12)
-                        ghat = norm / (1.0 - norm).clamp_min(1e-6)
-                    ghat = ghat * value_spread.to(ghat.dtype)
-            else:
-                ghat = torch.zeros(pos.shape, dtype=torch.float32, device=self.device)
-            return keep_select(pos, ghat.contiguous(), capacity, w, sink_tokens=cfg.sink_tokens,
-                               pin=self._pin_rows())
-        raise ValueError(f"policy {cfg.policy} does not evict")
+        """Live-axis indices of the `capacity` entries to keep in every lane, [L, B, Hkv, C],
+        in position order: the policy's contest solved by ma_keep_select."""
+        rank, window = self._contest(cfg, capacity, value_spread, score)
+        return keep_select(self._in_use("pos"), rank.contiguous(), capacity, window, sink_tokens=cfg.sink_tokens,
+                           pin=self._pin_rows())
 
     def _pin_rows(self):
+        """The pinned position range (lo, hi): lo an int or a per-sequence [B] tensor."""
         if self.pin is None:
             return None
         lo, hi = self.pin
         if isinstance(lo, torch.Tensor):
             lo = lo.to(self.device, torch.int64).view(1, -1, 1)
-        return (lo, hi)
+        return lo, hi
 
     def compact(self, keep: torch.Tensor) -> None:
-        """Drop everything outside ``keep`` [L, B, Hkv, C], in place (eviction.py:411-418)."""
-        c = keep.shape[-1]
-        lb = self.num_layers * self.batch_size
-        h = self.num_kv_heads
-        k3 = keep.reshape(lb, h, c)
-        planes = [t.view(lb, h, t.shape[-1], 1) for t in (self.g, self.n, self.pos, self.phys)]
-        compact_tokens(planes, k3, self.live)
+        """Keep the live rows keep [L, B, Hkv, C] of every column, in that order, in place."""
+        c = int(keep.shape[-1])
+        lanes, h = self.num_layers * self.batch_size, self.num_kv_heads
+        planes = [self._cols[name].view(lanes, h, self.rows, 1) for name in self._COLUMNS]
+        compact_tokens(planes, keep.reshape(lanes, h, c), self.live)
         self.live = c
 
     def maybe_evict(self, cfg: EvictionConfig, *, block_index: int, tokens_seen: int,
                     value_spread_fn: Callable[[], torch.Tensor] | None = None,
                     score_fn: Callable[[], torch.Tensor] | None = None) -> torch.Tensor | None:
-        """Evict on schedule (eviction.py:420-457); returns the survivors or None."""
-        if not cfg.enabled or self.live == 0 or cfg.policy == "snapkv":
-            return None
-        if (block_index + 1) % cfg.interval_blocks:
-            return None
+        """The end-of-block eviction of the EMA and scored policies (eviction.py:420-457):
+        every interval_blocks blocks, when more than cfg.capacity(tokens_seen) entries are
+        live, keep that many and compact; returns the keep set, or None when nothing ran.
+        SnapKV compresses the prompt only and never evicts here."""
+        due = cfg.enabled and cfg.policy != "snapkv" and (block_index + 1) % cfg.interval_blocks == 0
         capacity = cfg.capacity(tokens_seen)
-        if self.live <= capacity:
+        if not due or self.live <= capacity:
             return None
-        spread = None
+        spread = score = None
         if cfg.policy == "ema_recent_value":
             if value_spread_fn is None:
                 raise ValueError("policy ema_recent_value needs a value_spread_fn")
             spread = value_spread_fn()
-        score = None
-        if cfg.policy in ("expected_attention", "greedy_set", "oracle_future", "snapkv"):
+        if cfg.policy in ("expected_attention", "greedy_set", "oracle_future"):
             if score_fn is None:
                 raise ValueError(f"policy {cfg.policy} needs a score_fn")
             score = score_fn(capacity) if cfg.policy == "greedy_set" else score_fn()

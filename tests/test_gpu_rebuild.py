@@ -38,8 +38,6 @@ def _cache_from(store: dict, lens: tuple, dev, *, stage: bool = False, residual_
         t[:, :, :, :src.shape[3]] = src
         setattr(cache, name, t.to(dev))
     cache.length, cache.quantized_length, cache.residual_length, cache.dropped = lens
-    cache.capacity = cache.v_q.shape[3]
-    cache.residual_capacity = cache.k_residual.shape[3]
     cache.stage = stage
     return cache
 

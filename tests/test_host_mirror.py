@@ -32,18 +32,20 @@ def test_quantization_validate_messages():
 def test_cache_layouts_and_append_plan_cpu():
     c = PackedKVCache(num_layers=3, batch_size=2, num_kv_heads=4, head_dim=128, max_tokens=5000,
                       quant=QuantizationConfig(), device="cpu")
-    assert c.capacity == 1024 and c.residual_capacity == 63
-    assert tuple(c.k_q.shape) == (3, 2, 4, 32, 128, 16) and tuple(c.k_scale.shape) == (3, 2, 4, 32, 128)
-    assert tuple(c.v_q.shape) == (3, 2, 4, 1024, 4, 16) and tuple(c.v_scale.shape) == (3, 2, 4, 1024, 4)
+    cap, rcap = c.capacity, c.residual_capacity
+    assert cap % 32 == 0 and 32 <= cap <= 5024 and rcap >= 32 + 32    # a whole block beyond the residual fits
+    assert tuple(c.k_q.shape) == (3, 2, 4, cap // 32, 128, 16) and tuple(c.k_scale.shape) == (3, 2, 4, cap // 32, 128)
+    assert tuple(c.v_q.shape) == (3, 2, 4, cap, 4, 16) and tuple(c.v_scale.shape) == (3, 2, 4, cap, 4)
     assert c.k_scale.dtype == torch.float16 and c.k_fp is None
+    assert tuple(c.k_residual.shape) == (3, 2, 4, rcap, 128) and c.k_residual.dtype == torch.bfloat16
     plan = c.begin_append(1000)
     assert (plan.quantize_from_residual, plan.new_residual) == (960, 40)
     with pytest.raises(RuntimeError, match="already in progress"):
         c.begin_append(1)
     c.abort_append()
-    plan = c.begin_append(1500)                       # grows the storage past 1024
-    assert c.capacity >= 1536 and c.k_q.shape[3] == c.capacity // 32
-    assert (plan.quantize_from_residual, plan.new_residual) == (1440, 60)
+    plan = c.begin_append(4000)                       # grows the storage past its first allocation
+    assert c.capacity >= 4000 and c.k_q.shape[3] == c.capacity // 32 and c.v_q.shape[3] == c.capacity
+    assert (plan.quantize_from_residual, plan.new_residual) == (3968, 32)
     with pytest.raises(ValueError, match="shape mismatch"):
         c.stage_layer(0, torch.zeros(2, 4, 3, 128), torch.zeros(2, 4, 3, 128))
     with pytest.raises(RuntimeError, match="not staged"):
@@ -53,7 +55,13 @@ def test_cache_layouts_and_append_plan_cpu():
         c.begin_append(6000)
     b = PackedKVCache(num_layers=1, batch_size=1, num_kv_heads=2, head_dim=64, max_tokens=100,
                       quant=QuantizationConfig(k_bits=16, v_bits=16), device="cpu")
-    assert b.capacity == 100 and tuple(b.k_fp.shape) == (1, 1, 2, 100, 64) and b.k_q is None
+    assert b.capacity >= 100 and tuple(b.k_fp.shape) == (1, 1, 2, b.capacity, 64) and b.k_q is None
+    assert b.residual_capacity == 0 and b.k_residual is None
+    # accounting: nothing in use yet; every plane's bytes allocated
+    assert c.logical_nbytes()["total"] == 0
+    assert c.allocated_nbytes() == sum(t.numel() * t.element_size() for t in (c.k_q, c.k_scale, c.k_zero, c.v_q,
+                                                                               c.v_scale, c.v_zero, c.k_residual,
+                                                                               c.v_residual))
     with pytest.raises(KernelUnavailableError):
         PackedKVCache(num_layers=1, batch_size=1, num_kv_heads=2, head_dim=64, max_tokens=100,
                       quant=QuantizationConfig(), device="cpu", backend="torch")
