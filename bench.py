@@ -185,7 +185,7 @@ def main():
     q, k, v, kc, vc = layer_inputs(sh, dtype=torch.bfloat16)
     qg, kcg, vcg = q.to(dev), kc.to(dev), vc.to(dev)
     kdev, vdev = k.to(dev), v.to(dev)
-    rows = torch.arange(sh.t, dtype=torch.int32, device=dev)
+    rows = list(range(sh.t))          # the whole block in order (mode "all"), as the session passes it
 
     class View:
         """the packed cache of one layer, as the gather reads it (cache.py:LayerView)"""

@@ -136,6 +136,8 @@ int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, in
  * slots) and, when value != 0, score[j] = mass[j] * ||v_j - centre|| (0 on dead slots),
  * centre as ma_value_centre computes it from op (the prefix-only output of
  * ma_splitk_attention, [B,H,R,D] contiguous, dtype op_dtype; read only when value != 0).
+ * q_rows: int32 [T2] block positions of the selection rows, or NULL for positions 0 .. T2-1
+ * in order (T2 <= T; mode "all" is T2 = T).
  * v_round: 0, or MA_BF16 / MA_F16: the distance reads packed V rounded to that dtype (the
  * reference reads the prefix it unpacked to the query dtype when it has one,
  * splitk.py:513-516, 592).  mass/score [B,H,n] contiguous.  Mass-only calls take any number

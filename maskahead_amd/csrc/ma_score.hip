@@ -33,7 +33,6 @@ using namespace ma;
 namespace {
 
 constexpr int SNT = 1024;
-constexpr int SWAVES = SNT / 64;
 constexpr int MAX_RT = 16;       // row tiles of 32 selection rows
 constexpr int MAX_R2 = 32 * MAX_RT;
 enum { SRC_PACKED = 0, SRC_DENSE = 1 };
@@ -41,7 +40,8 @@ enum { SRC_PACKED = 0, SRC_DENSE = 1 };
 struct ScoreArgs {
     ma_tensor4 q;
     PrefixDev pre;
-    const int32_t *q_rows;
+    const int32_t *q_rows;   // NULL: the selection rows are block positions row0 .. row0 + T2 - 1
+    int row0;
     const float *mp, *lp;
     const void *op;  // prefix-only output [B*H, R, D] (op_dtype): the value centre's source
     int op_dtype;
@@ -59,15 +59,40 @@ struct ScoreArgs {
 // ------------------------------------------------------------------ value centre
 // centre[d] = (1/R2) * sum over rows r < R of cnt[r] * f32(op[bh, r, d]), cnt[r] = how many
 // of the R2 selection rows are row r (the mean of O_p over the selection rows).  SNT
-// threads: thread (slot s, chunk c) sums rows r = s, s + S, ... (ascending, rows with
-// cnt 0 skipped) of channels 8c..8c+7; slots are then summed in groups of 8, then the
-// groups -- one fixed order, shared by score_kernel and centre_kernel.
-template <int D>
+// threads: thread (slot s, chunk c) sums rows r = s, s + S, ... (ascending) of channels
+// 8c..8c+7; the slots of a wave are then summed by lane exchanges (partners at xor CH, 2 CH,
+// ...), and the NT / 64 wave sums in wave order -- one fixed order, shared by score_kernel
+// and centre_kernel.
+template <int D, int NT = SNT>
 struct CentreSmem {
-    static constexpr int CH = D / 8, S = SNT / CH, QG = SNT / D;
-    float part[S][D];
-    float part2[QG][D];
+    static constexpr int CH = D / 8, S = NT / CH;
+    float part[NT / 64][D];
 };
+
+// the slot sums acc[8] of this thread (slot tid / CH, chunk tid % CH) -> cen[0 .. D) in
+// LDS (visible to the block on return; cs and cen may be any LDS)
+template <int D, int NT>
+__device__ __forceinline__ void centre_reduce(float (&acc)[8], CentreSmem<D, NT> &cs, float *cen, int r2) {
+    constexpr int CH = D / 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int o = CH; o < 64; o *= 2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
+    }
+    if (lane < CH) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cs.part[wave][lane * 8 + e] = acc[e];
+    }
+    __syncthreads();
+    if (tid < D) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) t += cs.part[w][tid];
+        cen[tid] = t / (float)r2;
+    }
+    __syncthreads();
+}
 
 // the row of selection row rr: (rr / T2) * T + clamp(q_rows[rr % T2], 0, T - 1)
 __device__ __forceinline__ int sel_row(const int32_t *q_rows, int rr, int T2, int T, int *g_out, int *t_out) {
@@ -268,11 +293,11 @@ __device__ __forceinline__ float token_sum(float v) {
 
 constexpr int MAX_R = 1024;   // query rows of a KV head (G * T)
 
-template <int D>
+template <int D, int NT>
 struct ScoreSmem {
     union {
         KTileL<D> kt[2];
-        CentreSmem<D> cs;
+        CentreSmem<D, NT> cs;
     } u;
     float red[2][2 * MAX_RT][TILE / 2];  // per (row tile, 32-token half) unit: its token sums
     float dist[3][TILE];
@@ -286,12 +311,16 @@ struct ScoreSmem {
 };
 
 // Every wave does both jobs, in lock step: S units (a 32-row tile x a 32-token half of a
-// tile, or both halves when the selection needs more than 8 row tiles) and staging items
-// (thread t stages item t: K items [0, 4D), then V items [4D, 8D)).  HALVES: token halves
-// per S unit.
-template <int D, int SRC, int HALVES>
-__global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
-    __shared__ ScoreSmem<D> sm;
+// tile, or both halves) and staging items (thread t stages items t, t + NT, ...: K items
+// [0, 4D), then V items [4D, 8D)).  HALVES: token halves per S unit.  NT = 1024 (one
+// workgroup per CU, units of half a tile for up to 16 row tiles) or 512 (two workgroups per
+// CU, so one's memory waits overlap the other's work; up to 8 row tiles, whole-tile units,
+// every thread stages one K item and one V item).
+template <int D, int SRC, int HALVES, int NT>
+__global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
+    __shared__ ScoreSmem<D, NT> sm;
+    constexpr int NWV = NT / 64;                       // waves
+    constexpr int IPT = 8 * D > NT ? 8 * D / NT : 1;   // staging items per thread
     constexpr int KS = D + 8;
     constexpr int NKS = D / 16;
     constexpr int NIK = 4 * D;                         // K items per tile
@@ -318,9 +347,10 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
 
     // ---- fast staging state: this thread's item offsets inside a tile, once
     const int ni = value ? 2 * NIK : NIK;              // staging items per tile
-    const bool has_item = tid < ni;
-    uint32_t w[NW];
-    uint2 off = uint2{0u, 0u};
+    uint32_t w[IPT][NW];
+    uint2 off[IPT];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) off[j] = uint2{0u, 0u};
     const uint8_t *kq0 = nullptr, *vq0 = nullptr;
     const uint16_t *ks0 = nullptr, *kz0 = nullptr, *vs0 = nullptr, *vz0 = nullptr;
     const char *kf0 = nullptr, *vf0 = nullptr;
@@ -328,9 +358,13 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
     int kq_d = 0;
     if (fast) {
         const Lane L = make_lane(a.pre, b, h, bh);
-        if (tid < NIK) off = SRC == SRC_PACKED ? kp_offsets<D>(L, tid) : uint2{kd_offset<D>(L, tid), 0u};
-        else if (has_item)
-            off = SRC == SRC_PACKED ? vp_offsets<D>(L, tid - NIK) : uint2{vd_offset<D>(L, tid - NIK), 0u};
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int u = tid + j * NT;
+            if (u < NIK) off[j] = SRC == SRC_PACKED ? kp_offsets<D>(L, u) : uint2{kd_offset<D>(L, u), 0u};
+            else if (u < ni)
+                off[j] = SRC == SRC_PACKED ? vp_offsets<D>(L, u - NIK) : uint2{vd_offset<D>(L, u - NIK), 0u};
+        }
         kq0 = L.kq;
         ks0 = L.ks;
         kz0 = L.kz;
@@ -350,19 +384,28 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
     // this thread's item of tile i of the run into w
     auto load = [&](int i) {
         const int64_t ti = tile0 + i;   // whole tiles: packed tile ti starts at key group 2*ti
-        if (tid < NIK) {
-            if constexpr (SRC == SRC_PACKED) kp_load(w, kq0 + ti * kq_tile, ks0 + ti * ks_tile, kz0 + ti * ks_tile, kq_d, off);
-            else d32_load(w, kf0 + ti * kf_tile, off.x);
-        } else if (has_item) {
-            if constexpr (SRC == SRC_PACKED) vp_load(w, vq0 + ti * vq_tile, vs0 + ti * vs_tile, vz0 + ti * vs_tile, off);
-            else d32_load(w, vf0 + ti * vf_tile, off.x);
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int u = tid + j * NT;
+            if (u < NIK) {
+                if constexpr (SRC == SRC_PACKED)
+                    kp_load(w[j], kq0 + ti * kq_tile, ks0 + ti * ks_tile, kz0 + ti * ks_tile, kq_d, off[j]);
+                else d32_load(w[j], kf0 + ti * kf_tile, off[j].x);
+            } else if (u < ni) {
+                if constexpr (SRC == SRC_PACKED)
+                    vp_load(w[j], vq0 + ti * vq_tile, vs0 + ti * vs_tile, vz0 + ti * vs_tile, off[j]);
+                else d32_load(w[j], vf0 + ti * vf_tile, off[j].x);
+            }
         }
     };
 
     // ---- prologue: the first tile's loads, q_rows and M_p / L_p of every row at once, then
     // the selection-row tables from LDS, then Q and the value centre
     if (fast) load(0);
-    if (tid < T2) sm.qr[tid] = a.q_rows[tid];
+    // in-order selection rows (the whole block, mode "all"): every table below is arithmetic,
+    // so M_p / L_p, Q and the centre's rows are loaded in the first round trip
+    const bool ident = a.q_rows == nullptr;
+    if (!ident && tid < T2) sm.qr[tid] = a.q_rows[tid];
     // exp(s - M) / L == exp2(s*log2e - (M*log2e + log2 L)); rows without a live prefix
     // entry (L = 0) and padding rows contribute exactly 0.  Up to MAX_R rows per KV head the
     // constants of every row come in the same round trip as q_rows; beyond (long prefill
@@ -372,96 +415,128 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
         const float m = a.mp[(int64_t)bh * R + r], l = a.lp[(int64_t)bh * R + r];
         return l > 0.f ? __builtin_fmaf(m, MA_LOG2E, __log2f(l)) : __builtin_inff();
     };
-    if (row_table) {
-        for (int r = tid; r < R; r += SNT) sm.rowc[r] = row_const(r);
-        for (int r = tid; r < MAX_R; r += SNT) sm.cnt[r] = 0;
-    }
-    __syncthreads();
+    // selection row rr = g * T2 + i: block position t (clamped into the block), row g * T + t
+    auto sel_pos = [&](int rr, int g) {
+        return min(max(ident ? a.row0 + rr - g * T2 : sm.qr[rr - g * T2], 0), T - 1);
+    };
     const int rt_pad = 32 * row_tiles;
-    for (int rr = tid; rr < rt_pad; rr += SNT) {
-        float c = __builtin_inff();
-        int row = 0, qo = -1;
-        if (rr < R2) {
-            const int g = rr / T2;
-            const int t = min(max(sm.qr[rr - g * T2], 0), T - 1);   // as sel_row
-            row = g * T + t;
-            qo = g * (int)a.q.s[1] + t * (int)a.q.s[2];
-            if (row_table) {
-                atomicAdd(&sm.cnt[row], 1);
-                c = sm.rowc[row];
-            } else {
+    if (ident) {
+        for (int rr = tid; rr < rt_pad; rr += NT) {
+            float c = __builtin_inff();
+            int row = 0, qo = -1;
+            if (rr < R2) {
+                const int g = rr / T2, t = sel_pos(rr, g);
+                row = g * T + t;
+                qo = g * (int)a.q.s[1] + t * (int)a.q.s[2];
                 c = row_const(row);
             }
+            sm.crow[rr] = c;
+            sm.rrow[rr] = row;
+            sm.qoff[rr] = qo;
         }
-        sm.crow[rr] = c;
-        sm.rrow[rr] = row;
-        sm.qoff[rr] = qo;
+    } else {
+        if (row_table) {
+            for (int r = tid; r < R; r += NT) sm.rowc[r] = row_const(r);
+            for (int r = tid; r < MAX_R; r += NT) sm.cnt[r] = 0;
+        }
+        __syncthreads();
+        for (int rr = tid; rr < rt_pad; rr += NT) {
+            float c = __builtin_inff();
+            int row = 0, qo = -1;
+            if (rr < R2) {
+                const int g = rr / T2, t = sel_pos(rr, g);
+                row = g * T + t;
+                qo = g * (int)a.q.s[1] + t * (int)a.q.s[2];
+                if (row_table) {
+                    atomicAdd(&sm.cnt[row], 1);
+                    c = sm.rowc[row];
+                } else {
+                    c = row_const(row);
+                }
+            }
+            sm.crow[rr] = c;
+            sm.rrow[rr] = row;
+            sm.qoff[rr] = qo;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     bf16x8_t qf[NKS];
     if (s_wave) {
-        const int qo = sm.qoff[rt * 32 + c32];
+        int qo;
+        if (ident) {
+            const int rr = rt * 32 + c32, g = rr / T2;
+            qo = rr < R2 ? g * (int)a.q.s[1] + sel_pos(rr, g) * (int)a.q.s[2] : -1;
+        } else {
+            qo = sm.qoff[rt * 32 + c32];
+        }
         const int64_t qb = b * a.q.s[0] + (int64_t)h * a.G * a.q.s[1] + (qo < 0 ? 0 : qo);
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[ks] = qo < 0 ? bf16x8_t{} : qf[ks];
     }
 
     // value centre: centre[d] = (1/R2) * sum over rows r of cnt[r] * f32(O_p[r][d]), rows of
     // a slot in ascending order, then slots in groups of 8, then the groups
     if (value) {
-        using CS = CentreSmem<D>;
         const int osl = tid / CH, och = tid % CH;
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-        for (int r = osl; r < R; r += SNT / CH) {
-            const int n = sm.cnt[r];
-            if (n > 0) {
-                const int64_t off_o = ((int64_t)bh * R + r) * D + och * 8;
-                float x[8];
-                if (a.op_dtype == MA_F32) {
-                    const f32x4_t *pp = (const f32x4_t *)((const float *)a.op + off_o);
-                    const f32x4_t x0 = pp[0], x1 = pp[1];
+        // rows osl, osl + S, ... of channels 8 och .. 8 och + 7, in batches of CB rows whose
+        // loads are in flight together; a row counts as often as it is a selection row (in
+        // order: every row once); rows past R count 0 (their address is clamped)
+        constexpr int CB = 4;
+        constexpr int S = NT / CH;
+        for (int r0 = osl; r0 < R; r0 += CB * S) {
+            uint4 raw[CB];
+            float wgt[CB];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        x[e] = x0[e];
-                        x[4 + e] = x1[e];
-                    }
+            for (int j = 0; j < CB; ++j) {
+                const int r = r0 + j * S;
+                const int tpos = r % T - a.row0;
+                wgt[j] = r >= R ? 0.f : ident ? (tpos >= 0 && tpos < T2 ? 1.f : 0.f) : (float)sm.cnt[r];
+                const int64_t off_o = ((int64_t)bh * R + min(r, R - 1)) * D + och * 8;
+                if (a.op_dtype == MA_F32) {
+                    raw[j] = *(const uint4 *)((const float *)a.op + off_o);
                 } else {
-                    const uint4 v4 = *(const uint4 *)((const uint16_t *)a.op + off_o);
-                    const uint32_t wv[4] = {v4.x, v4.y, v4.z, v4.w};
-                    const bool bf = a.op_dtype == MA_BF16;
+                    raw[j] = *(const uint4 *)((const uint16_t *)a.op + off_o);
+                }
+            }
+            if (a.op_dtype == MA_F32) {
+                // f32 rows: the second half of the 8 channels (the first came with raw[j])
+                uint4 hi[CB];
+#pragma unroll
+                for (int j = 0; j < CB; ++j)
+                    hi[j] = *(const uint4 *)((const float *)a.op +
+                                             ((int64_t)bh * R + min(r0 + j * S, R - 1)) * D + och * 8 + 4);
+#pragma unroll
+                for (int j = 0; j < CB; ++j) {
+                    const uint32_t wv[8] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[e] += wgt[j] * __uint_as_float(wv[e]);
+                }
+            } else {
+                const bool bf = a.op_dtype == MA_BF16;
+#pragma unroll
+                for (int j = 0; j < CB; ++j) {
+                    const uint32_t wv[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const uint16_t hx = (uint16_t)(wv[e >> 1] >> ((e & 1) * 16));
-                        x[e] = bf ? ma_bf16_to_f32(hx) : ma_f16_to_f32(hx);
+                        acc[e] += wgt[j] * (bf ? ma_bf16_to_f32(hx) : ma_f16_to_f32(hx));
                     }
                 }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] += (float)n * x[e];
             }
         }
-        CS &cs = sm.u.cs;
+        centre_reduce<D, NT>(acc, sm.u.cs, sm.cen, R2);
+    }
+    if (s_wave) {
+        // padding rows of the last row tile: zero queries (applied only now, so that the Q
+        // loads and the centre's loads are in flight together)
+        const int rr = rt * 32 + c32;
+        if (rr >= R2) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) cs.part[osl][och * 8 + e] = acc[e];
-        __syncthreads();
-        {
-            const int d = tid % D, q = tid / D;
-            float t = 0.f;
-#pragma unroll
-            for (int k = 0; k < CS::S / CS::QG; ++k) t += cs.part[q * (CS::S / CS::QG) + k][d];
-            cs.part2[q][d] = t;
+            for (int ks = 0; ks < NKS; ++ks) qf[ks] = bf16x8_t{};
         }
-        __syncthreads();
-        if (tid < D) {
-            float t = 0.f;
-#pragma unroll
-            for (int q = 0; q < CS::QG; ++q) t += cs.part2[q][tid];
-            sm.cen[tid] = t / (float)R2;
-        }
-        __syncthreads();
     }
 
     // ---- S unit: tile in K buffer kb into the unit's token sums red[rb]
@@ -511,42 +586,48 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
         const int n0 = tile0 * TILE;
         uint16_t *Ks = sm.u.kt[0].k;
 #pragma unroll 1
-        for (int it = tid; it < TILE * D; it += SNT) {
+        for (int it = tid; it < TILE * D; it += NT) {
             const int t = it / D, d = it % D;
             const int j = n0 + t;
             Ks[t * KS + d] = ma_f32_to_bf16(j < end ? lane_key(L, j, d) : 0.f);
         }
         if (value) {
-            // V items (token, 16 channels): one per thread, the D/16 lanes of a token adjacent
-            const int v = tid;
-            float dd = v < NIK ? vg_dist<D>(L, v, n0, end, &sm.cen[(v % TPI) * 16], a.vround) : 0.f;
-            dd = token_sum<D>(dd);
-            if (v < NIK && v % TPI == 0) sm.dist[0][v / TPI] = dd;
+            // V items (token, 16 channels), the D/16 lanes of a token adjacent
+            for (int v0 = 0; v0 < NIK; v0 += NT) {
+                const int v = v0 + tid;
+                float dd = v < NIK ? vg_dist<D>(L, v, n0, end, &sm.cen[(v % TPI) * 16], a.vround) : 0.f;
+                dd = token_sum<D>(dd);
+                if (v < NIK && v % TPI == 0) sm.dist[0][v / TPI] = dd;
+            }
         }
         __syncthreads();
         if (s_wave) s_tile(0, 0);
         __syncthreads();
-        if (wave == SWAVES - 1) finish(tile0, 0, 0);
+        if (wave == NWV - 1) finish(tile0, 0, 0);
         return;
     }
 
     // ---- fast workgroup: this thread's item of the tile in w into K buffer kb and
     // distance buffer db
     const int vround = a.vround;
-    const float *cen16 = &sm.cen[(has_item && tid >= NIK ? (tid - NIK) % TPI : 0) * 16];
     auto stage = [&](int kb, int db) {
         uint16_t *Ks = sm.u.kt[kb].k;
-        if (tid < NIK) {
-            if constexpr (SRC == SRC_PACKED) kp_store<D>(Ks, w, tid);
-            else kd_store<D>(Ks, w, tid, a.pre.fdtype);
-        } else if (value && tid < NIK + NIK) {
-            float dd = 0.f;
-            if constexpr (SRC == SRC_PACKED)
-                dd = vround == MA_BF16 ? vp_dist<MA_BF16>(w, cen16)
-                                       : (vround == MA_F16 ? vp_dist<MA_F16>(w, cen16) : vp_dist<0>(w, cen16));
-            else dd = vd_dist(w, cen16, a.pre.fdtype);
-            dd = token_sum<D>(dd);
-            if ((tid - NIK) % TPI == 0) sm.dist[db][(tid - NIK) / TPI] = dd;
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int u = tid + j * NT;
+            if (u < NIK) {
+                if constexpr (SRC == SRC_PACKED) kp_store<D>(Ks, w[j], u);
+                else kd_store<D>(Ks, w[j], u, a.pre.fdtype);
+            } else if (value && u < NIK + NIK) {
+                const float *cen16 = &sm.cen[((u - NIK) % TPI) * 16];
+                float dd = 0.f;
+                if constexpr (SRC == SRC_PACKED)
+                    dd = vround == MA_BF16 ? vp_dist<MA_BF16>(w[j], cen16)
+                                           : (vround == MA_F16 ? vp_dist<MA_F16>(w[j], cen16) : vp_dist<0>(w[j], cen16));
+                else dd = vd_dist(w[j], cen16, a.pre.fdtype);
+                dd = token_sum<D>(dd);
+                if ((u - NIK) % TPI == 0) sm.dist[db][(u - NIK) / TPI] = dd;
+            }
         }
     };
 
@@ -562,10 +643,10 @@ __global__ void __launch_bounds__(SNT) score_kernel(ScoreArgs a) {
             if (i + 2 < ntiles) load(i + 2);
         }
         // tile i - 1 is complete in LDS since the last barrier
-        if (wave == SWAVES - 1 && i > 0) finish(tile0 + i - 1, (i - 1) & 1, (i - 1) % 3);
+        if (wave == NWV - 1 && i > 0) finish(tile0 + i - 1, (i - 1) & 1, (i - 1) % 3);
         __syncthreads();
     }
-    if (wave == SWAVES - 1) finish(tile0 + ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) % 3);
+    if (wave == NWV - 1) finish(tile0 + ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) % 3);
 }
 
 // the value centre of prefix_scores alone (same definition and order as score_kernel)
@@ -597,23 +678,9 @@ __global__ void __launch_bounds__(SNT) centre_kernel(const void *op, int op_dtyp
             for (int e = 0; e < 8; ++e) acc[e] += (float)n * ma_load_f(op, off_o + e, op_dtype);
         }
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) cs.part[osl][och * 8 + e] = acc[e];
-    __syncthreads();
-    {
-        const int d = tid % D, q = tid / D;
-        float t = 0.f;
-#pragma unroll
-        for (int k = 0; k < CS::S / CS::QG; ++k) t += cs.part[q * (CS::S / CS::QG) + k][d];
-        cs.part2[q][d] = t;
-    }
-    __syncthreads();
-    if (tid < D) {
-        float t = 0.f;
-#pragma unroll
-        for (int q = 0; q < CS::QG; ++q) t += cs.part2[q][tid];
-        centre[(int64_t)bh * D + tid] = t / (float)R2;
-    }
+    __shared__ float cen[D];
+    centre_reduce<D, SNT>(acc, cs, cen, R2);
+    if (tid < D) centre[(int64_t)bh * D + tid] = cen[tid];
 }
 
 }  // namespace
@@ -651,8 +718,8 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     const char *who = "ma_prefix_scores";
     int rc = ma_validate_prefix(p, D, who);
     if (rc) return rc;
-    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || T2 <= 0 || !q.ptr || !q_rows || !mp || !lp || !mass ||
-        (value && (!score || !op))) {
+    if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || T2 <= 0 || !q.ptr || (!q_rows && T2 > T) || !mp || !lp ||
+        !mass || (value && (!score || !op))) {
         ma_set_error("%s: bad sizes or NULL pointer", who);
         return MA_EINVAL;
     }
@@ -687,7 +754,12 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
                                              p->skf[0] % 16 == 0 && p->skf[1] % 16 == 0 && p->svf[0] % 16 == 0 &&
                                              p->svf[1] % 16 == 0);
     const int row_tiles_max = (G * t2_pass + 31) / 32;
+    // one 1024-thread workgroup per CU: units of half a tile up to 8 row tiles, whole
+    // tiles beyond.  (Two 512-thread workgroups per CU, NT = 512, measured 1.6x slower at
+    // config 2: each workgroup loads its lane's Q and O_p rows in its prologue, so twice
+    // the workgroups move twice those bytes.)
     const int halves = row_tiles_max <= 8 ? 1 : 2;
+    const int wgs_per_cu = 1;
     const int tiles = (n + TILE - 1) / TILE;
     const bool packed = p->nq > 0;
     // whole tiles of the source kind go to the pipelined workgroups, the rest (a tile
@@ -695,7 +767,8 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     // f32 or unaligned 16-bit prefixes) to one tail workgroup each
     int nfast = packed ? p->nq / TILE : n / TILE;
     if (!dense_vec_ok) nfast = 0;
-    int per = nfast > 0 ? (nfast * B * H + ma_num_cus() - 1) / ma_num_cus() : 1;
+    const int slots = wgs_per_cu * ma_num_cus();
+    int per = nfast > 0 ? (nfast * B * H + slots - 1) / slots : 1;
     if (per < 1) per = 1;
     const int fast_wgs = nfast > 0 ? (nfast + per - 1) / per : 0;
     ScoreArgs sa;
@@ -724,9 +797,8 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     sa.fast_wgs = fast_wgs;
     sa.sl2 = scale * MA_LOG2E;
     dim3 grid(fast_wgs + (tiles - nfast), B * H);
-    dim3 block(SNT);
     hipStream_t st = (hipStream_t)stream;
-#define MA_SCORE(D_, S_, H_) hipLaunchKernelGGL((score_kernel<D_, S_, H_>), grid, block, 0, st, sa)
+#define MA_SCORE(D_, S_, H_) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT>), grid, dim3(SNT), 0, st, sa)
 #define MA_SCORE_I(D_, S_)                        \
     do {                                          \
         if (halves == 1) MA_SCORE(D_, S_, 1);     \
@@ -734,7 +806,8 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     } while (0)
     for (int t0 = 0; t0 < T2; t0 += t2_pass) {
         const int t2 = T2 - t0 < t2_pass ? T2 - t0 : t2_pass;
-        sa.q_rows = q_rows + t0;
+        sa.q_rows = q_rows ? q_rows + t0 : nullptr;
+        sa.row0 = t0;
         sa.T2 = t2;
         sa.R2 = G * t2;
         sa.row_tiles = (G * t2 + 31) / 32;

@@ -206,7 +206,9 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
                   block_m: int = 64, block_n: int = 64):
     """Per prefix entry: mass a_j (mean prefix-softmax over the selection rows) and, with
     value=True, a_j * ||v_j - c|| with c the mean of O_p over those rows
-    (splitk.py:582-614).  q_rows: int32 block positions of the selection queries.
+    (splitk.py:582-614).  q_rows: block positions of the selection queries -- an int
+    tensor (on the GPU: used as given) or a host sequence / CPU tensor (checked; the whole
+    block in order takes the kernels' row-table-free path).
     Returns (mass, score) as [B, Hkv, n] f32 (score None when value=False); dead slots 0."""
     b, hq, t, d = query.shape
     mp, lp, op, used = stats
@@ -215,10 +217,18 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
     g = hq // hkv
     n = prefix.n
     prefix.check_mask(b, hkv)
-    if not q_rows.is_cuda and q_rows.numel() and (int(q_rows.min()) < 0 or int(q_rows.max()) >= t):
-        raise ValueError(f"q_rows must be block positions in [0, {t})")
-    q_rows = q_rows.to(device=query.device, dtype=torch.int32).contiguous()   # device rows: clamped in-kernel
-    t2 = int(q_rows.numel())
+    # host-side rows (a sequence, or a CPU tensor) are checked here; 0 .. T2-1 in order
+    # needs no row table at all (mode "all"); device rows are clamped into the block in-kernel
+    if not isinstance(q_rows, torch.Tensor) or not q_rows.is_cuda:
+        host = [int(x) for x in (q_rows.tolist() if isinstance(q_rows, torch.Tensor) else q_rows)]
+        if any(x < 0 or x >= t for x in host):
+            raise ValueError(f"q_rows must be block positions in [0, {t})")
+        q_rows = None if host == list(range(len(host))) else \
+            torch.tensor(host, dtype=torch.int32).to(query.device, non_blocking=True)
+        t2 = len(host)
+    else:
+        q_rows = q_rows.to(dtype=torch.int32).contiguous()
+        t2 = int(q_rows.numel())
     if t2 == 0:
         raise ValueError("q_rows cannot be empty")
     mass = torch.empty((b, hkv, n), device=query.device, dtype=torch.float32)
@@ -231,7 +241,7 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
         raise ValueError("stats O_p must be a contiguous [B, Hkv, R, D] tensor")
     scale = float(scaling) if scaling is not None else d ** -0.5
     vround = int(prefix.vround) if prefix.nq else 0
-    rc = lib.ma_prefix_scores(N.t4(query), b, hq, t, d, prefix.native(), hkv, q_rows.data_ptr(), t2,
+    rc = lib.ma_prefix_scores(N.t4(query), b, hq, t, d, prefix.native(), hkv, N.ptr(q_rows), t2,
                               mp.data_ptr(), lp.data_ptr(), op.data_ptr() if value else None,
                               N.dtype_code(op.dtype) if value else 0, scale, 1 if value else 0, vround,
                               mass.data_ptr(), N.ptr(score), st)

@@ -125,9 +125,13 @@ class FastLayerPath:
         pre.mask = self.slot_masks.get(layer_idx)
         return pre
 
-    def rows(self, positions) -> torch.Tensor:
-        """int32 device tensor of block positions, cached per distinct list (session.py:1369-1376)."""
+    def rows(self, positions):
+        """The selection rows to hand prefix_scores (session.py:1369-1376): positions 0 .. n-1
+        in order stay a host list (the score kernels need no row table for them); any other
+        list becomes an int32 device tensor, cached per distinct list."""
         key = tuple(int(p) for p in positions)
+        if key == tuple(range(len(key))):
+            return list(key)
         if self._rows_cache is None or self._rows_cache[0] != key:
             t = torch.tensor(key, dtype=torch.int32).to(self.cache.device, non_blocking=True)
             self._rows_cache = (key, t)
