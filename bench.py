@@ -54,7 +54,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall-clock budget of the CPU baseline sample (repeated whole steps)")
-    ap.add_argument("--eager", action="store_true", help="also time the step without the HIP graph")
+    ap.add_argument("--eager-steps", type=int, default=3,
+                    help="steps of the same workload timed without the HIP graph (0: skip)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the extra workloads of the default line (config 1 block step, config 3 keep "
+                         "step, 28-layer packed eviction)")
     ap.add_argument("--workload", choices=("step0", "evict", "substep"), default="step0",
                     help="step0: the headline read step (default); evict: the packed lazy eviction of all "
                          "28 layers (state compaction, rebuild plan, rebuild); substep: the denoising "
@@ -231,41 +235,54 @@ def main():
     ms_step, _ = time_graph(step, a.steps, a.warmup)
     ms_layer = ms_step / a.layers
 
-    # The two large kernels of the step, each alone in its own graph of INNER launches
-    # with the same arguments: split-K pass 1 and the value-aware score pass.
+    # The two large kernels of the step, each alone in a graph that launches it once per
+    # layer on that layer's own cache (as cold as in the step: the layers' caches together
+    # exceed the 256 MB Infinity Cache): split-K pass 1 and the value-aware score pass.
     lib = N.load()
     hq, t, d, hkv = sh.hq, sh.t, sh.d, sh.hkv
     ws_bytes = int(lib.ma_splitk_workspace_bytes(sh.b, hkv, hq, t, d, sh.n, 0, a.split_tokens))
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
-    pre_native = prefix.native()
+    natives = [L["prefix"].native() for L in layers]
     qt, kct, vct = N.t4(qg), N.t4(kcg), N.t4(vcg)
 
-    def partial():
-        N.check(lib.ma_splitk_partial(qt, sh.b, hq, t, d, pre_native, hkv, kct, vct, t, 0, 0, 0, d ** -0.5,
-                                      a.split_tokens, ws.data_ptr(), ws_bytes,
-                                      torch.cuda.current_stream().cuda_stream), "ma_splitk_partial")
+    def partial_all():
+        st = torch.cuda.current_stream().cuda_stream
+        for pn in natives:
+            N.check(lib.ma_splitk_partial(qt, sh.b, hq, t, d, pn, hkv, kct, vct, t, 0, 0, 0, d ** -0.5,
+                                          a.split_tokens, ws.data_ptr(), ws_bytes, st), "ma_splitk_partial")
 
-    out0, stats0 = splitk_attention(qg, prefix, kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
+    stats_all = [splitk_attention(qg, L["prefix"], kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)[1]
+                 for L in layers]
 
-    def scores_only():
-        prefix_scores(qg, prefix, stats0, rows, value=True)
+    def scores_all(q_rows=rows):
+        for L, stl in zip(layers, stats_all):
+            prefix_scores(qg, L["prefix"], stl, q_rows, value=True)
 
-    inner = 10
-    ms_partial, _ = time_graph(partial, a.steps, a.warmup, inner)
-    ms_scores, _ = time_graph(scores_only, a.steps, a.warmup, inner)
+    ms_partial = time_graph(partial_all, a.steps, a.warmup)[0] / a.layers
+    ms_scores = time_graph(scores_all, a.steps, a.warmup)[0] / a.layers
+    # the score pass with one and two selection positions (7 and 14 rows per KV head): the
+    # GQA-reduced VALU variant and the padded 32-row MFMA variant, each forced
+    variants = {}
+    for pos in ([sh.t - 1], [sh.t - 2, sh.t - 1]):
+        for name, mode in (("valu", 2), ("mfma", 1)):
+            prev_path = lib.ma_prefix_scores_path(mode)
+            try:
+                variants[(len(pos), name)] = time_graph(lambda: scores_all(pos), a.steps, a.warmup)[0] / a.layers
+            finally:
+                lib.ma_prefix_scores_path(prev_path)
+    del stats_all
 
     ms_eager = None
-    if a.eager:
-        for _ in range(a.warmup):
-            step()
+    if a.eager_steps > 0:
+        step()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(a.steps):
+        for _ in range(a.eager_steps):
             step()
         e1.record()
         torch.cuda.synchronize()
-        ms_eager = e0.elapsed_time(e1) / a.steps / a.layers
+        ms_eager = e0.elapsed_time(e1) / a.eager_steps / a.layers
 
     alg = algorithmic(sh)
     t_step = ms_layer * 1e-3
@@ -317,8 +334,24 @@ def main():
         "stages_us": {kk: round(v["ms"] * 1e3, 3) for kk, v in kernels.items()},
         "roofline": roof,
     }
+    g = sh.hq // sh.hkv
+    line["score_variants"] = {
+        f"r2_{npos * g}": {"rows": f"{npos} selection position(s) x {g} query heads per KV head",
+                           "valu_us": round(variants[(npos, "valu")] * 1e3, 3),
+                           "mfma_padded_us": round(variants[(npos, "mfma")] * 1e3, 3),
+                           "valu_hbm_frac": round(alg["pass2_bytes"] / (variants[(npos, "valu")] * 1e-3) / 1e9
+                                                  / HBM_PEAK_GBS, 4)}
+        for npos in (1, 2)}
     if ms_eager is not None:
+        # the same layer step launched op by op from Python (ctypes argument packing and
+        # torch allocations on every call), as a session without graph capture runs it
         line["eager_us_per_step"] = round(ms_eager * 1e3, 3)
+        line["eager_hbm_frac"] = round(alg["bytes"] / (ms_eager * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if not a.no_extras:
+        del layers, result
+        torch.cuda.empty_cache()
+        line["extras"] = {"c1_block_step": extra_c1_block(a), "c3_keep_step": extra_c3_keep(a),
+                          "evict_28_layers": extra_evict(a)}
     if not a.no_cpu:
         from oracle import attention as OA
 
@@ -407,6 +440,10 @@ def bench_substep(a):
 
 
 def bench_evict(a):
+    print(json.dumps(measure_evict(a, with_cpu=not a.no_cpu)), flush=True)
+
+
+def measure_evict(a, with_cpu):
     """The packed lazy eviction of every layer (session.py:270-361 + cache.py:236-335):
     28 layers x 4 KV heads of a 32 768-token int4 prefix + 32 bf16 residual tokens,
     keep 4 096 per lane (a 128-token recency window + a clustered seeded score), repack
@@ -446,7 +483,7 @@ def bench_evict(a):
     keep = score.topk(C, dim=-1).indices.sort(dim=-1).values.to(dev)
     names = ("k_q", "k_scale", "k_zero", "v_q", "v_scale", "v_zero", "k_residual", "v_residual")
     saved = {x: getattr(cache, x) for x in names}
-    meta = ("length", "quantized_length", "residual_length", "dropped", "capacity", "residual_capacity")
+    meta = ("length", "quantized_length", "residual_length", "dropped")   # capacities follow the planes
     saved_meta = {x: getattr(cache, x) for x in meta}
     pos0, phys0 = st.pos.clone(), st.phys.clone()
     cfg = EvictionConfig(policy="recent", recent_window=W, capacity_floor=W, compaction="lazy", repack_below=repack)
@@ -558,7 +595,7 @@ def bench_evict(a):
                      "kernel": "rebuild_kernel + remap_kernel", "avg_launch_us": round(us_rebuild, 2),
                      "algorithmic_bytes": rb_bytes},
     }
-    if not a.no_cpu:
+    if with_cpu:
         from oracle import rebuild as OR
 
         # bounded sample: 2 of the layers, the same lists, on the host
@@ -582,7 +619,160 @@ def bench_evict(a):
                                 "sample": f"{len(ctimes)} evictions of {Ls} of the {L} layers (oracle/rebuild.py, "
                                           f"torch CPU ops), median x {L // Ls}",
                                 "cpu": platform.processor() or platform.machine(), "os_cpu_count": os.cpu_count()}
-    print(json.dumps(line), flush=True)
+    return line
+
+
+def _roof(nbytes, flops, seconds):
+    """The roofline of a whole workload: HBM and MFMA fractions, bound = the larger floor."""
+    f_hbm = nbytes / seconds / 1e9 / HBM_PEAK_GBS
+    f_mfma = flops / seconds / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    hbm_bound = nbytes / HBM_PEAK_GBS / 1e9 >= flops / MFMA_BF16_PEAK_TFLOPS / 1e12
+    return {"bound": "hbm" if hbm_bound else "mfma",
+            "achieved": round(nbytes / seconds / 1e9, 2) if hbm_bound else round(flops / seconds / 1e12, 2),
+            "unit": "GB/s" if hbm_bound else "TFLOP/s", "frac": round(f_hbm if hbm_bound else f_mfma, 4),
+            "hbm_frac": round(f_hbm, 4), "mfma_frac": round(f_mfma, 4), "algorithmic_bytes": nbytes,
+            "algorithmic_flops": flops}
+
+
+def extra_c1_block(a):
+    """BASELINE config 1, one block step of every layer: step 0 over a bf16 prefix of
+    32 768 tokens (split-K attention with prefix statistics, value-aware scores, read-set
+    top-k of 2 048, gather into the compact buffer) and the block's 3 further denoising
+    sub-steps over [2 048 selected | block] (session.py:1403-1454, 1286-1336).  28 layers,
+    each with its own cache, in one HIP graph."""
+    from maskahead_amd.kernels import gather_packed_kv, prefix_scores, splitk_attention, topk_ascending
+    from maskahead_amd.kernels.splitk import Prefix
+    from maskahead_amd.workloads import CONFIGS, layer_inputs
+
+    sh, dev, subs = CONFIGS["c1"], torch.device("cuda:0"), 3
+    q, k, v, kc, vc = layer_inputs(sh, dtype=torch.bfloat16)
+    qg, kcg, vcg = q.to(dev), kc.to(dev), vc.to(dev)
+    kdev, vdev = k.to(dev), v.to(dev)
+    rows = list(range(sh.t))
+
+    class View:
+        """a bf16 cache layer, as the gather reads it"""
+        k_bits = v_bits = 16
+        quantized_length = residual_length = 0
+        key_token_group = value_channel_group = 32
+        k_q = k_scale = k_zero = v_q = v_scale = v_zero = k_residual = v_residual = None
+        head_dim = sh.d
+        key_mode = "channel"
+
+        def __init__(self, kf, vf):
+            self.k_fp, self.v_fp, self.length = kf, vf, kf.shape[2]
+
+    layers = []
+    for li in range(a.layers):
+        shift = (li * 977) % sh.n
+        kf = torch.roll(kdev, shift, dims=2).contiguous()
+        vf = torch.roll(vdev, shift, dims=2).contiguous()
+        ck = torch.empty((sh.b, sh.hkv, sh.read_k, sh.d), dtype=torch.bfloat16, device=dev)
+        layers.append((Prefix.dense(kf, vf), View(kf, vf), ck, torch.empty_like(ck)))
+    del kdev, vdev
+
+    def step():
+        for pre, view, ck, cv in layers:
+            _, stats = splitk_attention(qg, pre, kcg, vcg, want_prefix=True)
+            _, score = prefix_scores(qg, pre, stats, rows, value=True)
+            idx = topk_ascending(score, sh.read_k)
+            gather_packed_kv(view, idx, out_key=ck, out_value=cv)
+            sel = Prefix.dense(ck, cv)
+            for _ in range(subs):
+                splitk_attention(qg, sel, kcg, vcg)
+
+    ms = time_graph(step, max(5, a.steps // 5), 2)[0] / a.layers
+    r = (sh.hq // sh.hkv) * sh.t
+    kv = sh.n * sh.d * 2 * 2 * sh.hkv                       # bf16 K + V of the prefix
+    sel_kv = (sh.read_k + sh.t) * sh.d * 2 * 2 * sh.hkv
+    nbytes = (2 * kv + sh.n * sh.hkv * 8 + 2 * sh.read_k * sh.d * 2 * 2 * sh.hkv + subs * sel_kv)
+    flops = 4 * r * sh.n * sh.d * sh.hkv + 2 * r * sh.n * sh.d * sh.hkv + subs * 4 * r * (sh.read_k + sh.t) * sh.d * sh.hkv
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": f"{sh.name}: step 0 + {subs} sub-steps, bf16 prefix {sh.n}, read {sh.read_k}, "
+                        f"{a.layers} layers each with its own cache, one HIP graph",
+            "us_per_layer_block_step": round(ms * 1e3, 3), "roofline": _roof(nbytes, flops, ms * 1e-3)}
+
+
+def extra_c3_keep(a, layers=4, reps=5):
+    """BASELINE config 3, the look-ahead keep/evict step: per layer the probe forward of 96
+    queries (the block + 2 look-ahead blocks, block-causal) over a bf16 prefix of 65 536
+    tokens with their prefix mass, the keep score (value_score) and the keep set of 8 192
+    per KV head (128-token window, 4 sinks); then the in-place compaction of every layer
+    and the append of the finalized 32-token block (session.py:1985-2034, 2289-2297;
+    eviction.py:325-418; cache.py:342-367).  Launched op by op from Python, as the session
+    runs it; median of `reps` steps of `layers` layers, each from a restored cache."""
+    from maskahead_amd.cache import PackedKVCache
+    from maskahead_amd.config import QuantizationConfig
+    from maskahead_amd.kernels.keep import keep_select, value_score
+    from maskahead_amd.runtime.fastpath import FastLayerPath
+    from maskahead_amd.workloads import CONFIGS, layer_inputs
+
+    sh, dev = CONFIGS["c3"], torch.device("cuda:0")
+    q, k, v, kc, vc = layer_inputs(sh, dtype=torch.bfloat16)
+    qg, kcg, vcg = q.to(dev), kc.to(dev), vc.to(dev)
+    cache = PackedKVCache(num_layers=layers, batch_size=sh.b, num_kv_heads=sh.hkv, head_dim=sh.d,
+                          max_tokens=sh.n + 64, quant=QuantizationConfig(k_bits=16, v_bits=16), device=dev)
+    cache.begin_append(sh.n)
+    kdev, vdev = k.to(dev), v.to(dev)
+    for li in range(layers):
+        shift = (li * 977) % sh.n
+        cache.stage_layer(li, torch.roll(kdev, shift, dims=2), torch.roll(vdev, shift, dims=2))
+    cache.commit_append()
+    del kdev, vdev
+    saved = (cache.k_fp.clone(), cache.v_fp.clone())
+    meta = ("length", "quantized_length", "residual_length", "dropped")
+    saved_meta = {x: getattr(cache, x) for x in meta}
+    pos = torch.arange(sh.n, dtype=torch.int32, device=dev).expand(sh.b, sh.hkv, sh.n).contiguous()
+    fp = FastLayerPath(cache=cache, block_size=32, query_indices=list(range(32)))
+    blk_k, blk_v = kcg[:, :, :32].contiguous(), vcg[:, :, :32].contiguous()
+
+    def step():
+        keeps = []
+        for li in range(layers):
+            _, mass = fp.attend(li, qg, kcg, vcg, causal=32, q_pos0=sh.n, mass_rows=list(range(sh.t)))
+            score = value_score(mass, cache.layer_view(li).v_fp)
+            keeps.append(keep_select(pos, score, sh.keep_k, 128, sink_tokens=4, check=False))
+        cache.compact(torch.stack(keeps))
+        cache.begin_append(32)
+        for li in range(layers):
+            cache.stage_layer(li, blk_k, blk_v)
+        cache.commit_append()
+
+    times = []
+    for i in range(reps + 1):
+        cache.k_fp, cache.v_fp = saved[0].clone(), saved[1].clone()   # the step shrinks the planes
+        for x in meta:
+            setattr(cache, x, saved_meta[x])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        if i:
+            times.append(time.perf_counter() - t0)
+    sec = statistics.median(times) / layers
+    r = (sh.hq // sh.hkv) * sh.t
+    kv = sh.n * sh.d * 2 * sh.hkv                           # one bf16 plane (K or V) of the prefix
+    nbytes = (2 * kv + kv + kv + sh.n * sh.hkv * 4 * 3 + 2 * sh.keep_k * sh.d * 2 * 2 * sh.hkv
+              + 32 * sh.d * 2 * 2 * sh.hkv)
+    flops = 4 * r * sh.n * sh.d * sh.hkv + 2 * r * sh.n * sh.d * sh.hkv
+    del cache, saved
+    torch.cuda.empty_cache()
+    return {"workload": f"{sh.name}: probe of {sh.t} queries (block-causal) + prefix mass + value_score + keep "
+                        f"{sh.keep_k} of {sh.n} per KV head, compaction in place + append of 32 tokens; "
+                        f"{layers} layers, eager, median of {reps}",
+            "us_per_layer_keep_step": round(sec * 1e6, 1), "roofline": _roof(nbytes, flops, sec)}
+
+
+def extra_evict(a):
+    """The 28-layer packed lazy eviction (measure_evict), in short."""
+    import copy
+
+    b = copy.copy(a)
+    b.steps, b.warmup = min(a.steps, 10), 2
+    line = measure_evict(b, with_cpu=False)
+    torch.cuda.empty_cache()
+    return {"workload": line["config"]["workload"], "us_per_eviction": line["value"], "roofline": line["roofline"]}
 
 
 if __name__ == "__main__":

@@ -148,6 +148,17 @@ int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix 
                      int op_dtype, float scale, int value, int v_round, float *mass, float *score,
                      void *stream);
 
+/* a6v. The score pass of ma_prefix_scores for few selection rows per KV head (the
+ * reference serves every row count with BLOCK_M-row tl.dot tiles, splitk.py:321-371): a
+ * GQA-reduced VALU pass for at most 16 rows (G*T2 <= 16) -- waves stream 32-token units
+ * with no workgroup barrier, q . k by v_dot2c_f32_bf16 for every selection row, the value
+ * centre from those rows of O_p only -- instead of 32-row MFMA tiles that are mostly
+ * padding.  mode 0 (default) takes it for at most 8 rows (G 7 x T2 1, G 4 x T2 1-2) and
+ * the MFMA pass otherwise, 1 forces the MFMA pass, 2 the VALU pass (calls above 16 rows
+ * then fail); process-wide, for measurement and tests.  Returns the previous mode, or -1
+ * for a bad mode.  No counterpart in the reference (Triton picks no variant). */
+int ma_prefix_scores_path(int mode);
+
 /* a9. read-set top-k (session.py:1429-1438, reference.py:369-393): for each of `rows`
  * rows, the k largest of rank[row, 0..n) -- dead slots (mask 0) rank -inf, ties go to
  * the smaller index, -0.0 equals +0.0 and NaN ranks above +inf -- written as ascending

@@ -26,6 +26,8 @@
 // selection-row tables in LDS (row of every selection row, its query offset and c_r, one
 // load per row) and the value centre (mean of O_p over the selection rows, a fixed-order
 // LDS reduction shared with ma_value_centre).
+#include <atomic>
+
 #include "ma_stage.h"
 
 using namespace ma;
@@ -193,19 +195,22 @@ __device__ __forceinline__ void kd_store(uint16_t *Ks, const uint32_t *w, int u,
 }
 
 // V, packed: item u < 4D = (token t, 16-channel half hq of a 32-channel group), hq fastest
-// (the D/16 items of a token are adjacent lanes).  Words: 8 code bytes, f16 scale | zero.
+// (the D/16 items of a token are adjacent lanes).  Words: 8 code bytes, f16 scale, f16 zero.
 template <int D>
 __device__ __forceinline__ uint2 vp_offsets(const Lane &L, int u) {
     const int t = u / (D / 16), hq = u % (D / 16), cg = hq >> 1, ch = hq & 1;
     return uint2{(uint32_t)(t * L.vq_n + cg * L.vq_c + ch * 8), (uint32_t)(t * L.vs_n + cg)};
 }
 
+// (scale and zero stay in words of their own until use: combining them here would make the
+// wave wait for the loads where they are issued, one tile ahead)
 __device__ __forceinline__ void vp_load(uint32_t *w, const uint8_t *vq, const uint16_t *vs, const uint16_t *vz,
                                         uint2 o) {
     const uint2 x = *(const uint2 *)(vq + o.x);
     w[0] = x.x;
     w[1] = x.y;
-    w[2] = (uint32_t)vs[o.y] | ((uint32_t)vz[o.y] << 16);
+    w[2] = vs[o.y];
+    w[3] = vz[o.y];
 }
 
 // squared distance of the item's 16 channels to the centre (cen16: those channels, LDS);
@@ -213,7 +218,7 @@ __device__ __forceinline__ void vp_load(uint32_t *w, const uint8_t *vq, const ui
 // unpacked prefix, 0 = read as dequantized (f32)
 template <int VR>
 __device__ __forceinline__ float vp_dist(const uint32_t *w, const float *cen16) {
-    const float s = ma_f16_to_f32(w[2] & 0xffff), z = ma_f16_to_f32(w[2] >> 16);
+    const float s = ma_f16_to_f32((uint16_t)w[2]), z = ma_f16_to_f32((uint16_t)w[3]);
     float q[16];
     nib8(w[0], q);
     nib8(w[1], q + 8);
@@ -649,6 +654,268 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     if (wave == NWV - 1) finish(tile0 + ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) % 3);
 }
 
+// ------------------------------------------------------------------ GQA-reduced VALU pass
+// For at most SMALL_ROWS selection rows per KV head (a block position or two of a GQA
+// group) a 32-row MFMA tile would be mostly padding and score_kernel's per-workgroup
+// prologue (the value centre over every row of O_p, the row tables) would dominate.  Here
+// every wave streams its own run of 32-token units (one key group each); the workgroup
+// meets once, after a prologue that loads only the R2 selection rows' queries, their row
+// constants and the centre (the mean of O_p over those rows, in row order, as the
+// reference's index_select(...).mean(), splitk.py:598-601), while every wave's first unit
+// is already in flight:
+//   * staging: the unit's K is dequantized into the wave's LDS tile as bf16 [token][channel]
+//     (the same items and stores as score_kernel's K buffer); the V items give the
+//     squared distances to the centre straight from registers, one sum per token;
+//   * scores: lane (token t, channel half hh) forms q_r . k_t over its D/2 channels with
+//     v_dot2c_f32_bf16 for ROWS rows (R2 rounded up to 4, 8 or 16; the padding rows have
+//     zero queries and row constant +inf, so they add exactly 0), queries broadcast from
+//     LDS, adds the other half's sum (lane ^ 32) and sums exp2(s * scale*log2e - c_r);
+//   * the next unit's loads are issued before the scores of this one.
+constexpr int SMALL_ROWS = 16;
+constexpr int AUTO_SMALL_ROWS = 8;           // the largest row count mode 0 sends here
+constexpr int SM_NT = 256;                   // threads per workgroup
+constexpr int SM_WAVES = SM_NT / 64;
+constexpr int UNIT = KGRP;                   // tokens per unit
+
+template <int D>
+struct SmallSmem {
+    static constexpr int KS = D + 8;
+    uint16_t k[SM_WAVES][UNIT * KS];     // each wave's unit: bf16 K [token][channel]
+    float dist[SM_WAVES][UNIT];          // each wave's ||v - centre||^2 per token
+    uint4 qv[SMALL_ROWS][D / 8];         // the selection rows' queries, 8 bf16 per entry (padding 0)
+    float crow[SMALL_ROWS];              // per row: M_p*log2e + log2(L_p); +inf when L_p = 0 and for padding
+    float cen[D];
+};
+
+// LDS written by some lanes of a wave, then read by others of the same wave: LDS executes a
+// wave's accesses in order, so only the compiler must not move them across this point
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// KIND: 0 packed units, 1 16-bit units read with 16-byte loads, 2 element-wise (f32 or
+// unaligned 16-bit prefixes; no registers staged)
+template <int D>
+struct SmallWords {
+    static constexpr int NI = 2 * D / 64;   // K items and V items per lane and unit
+    uint32_t k[NI][8], v[NI][8];
+    uint2 ko[NI], vo[NI];
+};
+
+template <int D, int KIND>
+__device__ __forceinline__ void small_offsets(const Lane &L, SmallWords<D> &W) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < SmallWords<D>::NI; ++i) {
+        const int u = lane + 64 * i;
+        if constexpr (KIND == 0) {
+            W.ko[i] = kp_offsets<D>(L, u);
+            W.vo[i] = vp_offsets<D>(L, u);
+        } else if constexpr (KIND == 1) {
+            W.ko[i] = uint2{kd_offset<D>(L, u), 0u};
+            W.vo[i] = uint2{vd_offset<D>(L, u), 0u};
+        }
+    }
+}
+
+// unit uu's words of this lane; 16-bit units clamp tokens past the end (their results are
+// not written)
+template <int D, int KIND>
+__device__ __forceinline__ void small_load(const Lane &L, SmallWords<D> &W, int uu, int end, bool value) {
+    const int lane = threadIdx.x & 63;
+    const int j0 = uu * UNIT;
+    if constexpr (KIND == 0) {
+        const int g = j0 / KGRP;
+#pragma unroll
+        for (int i = 0; i < SmallWords<D>::NI; ++i) {
+            kp_load(W.k[i], L.kq + (int64_t)g * L.kq_g, L.ks + (int64_t)g * L.ks_g, L.kz + (int64_t)g * L.ks_g,
+                    L.kq_d, W.ko[i]);
+            if (value) vp_load(W.v[i], L.vq + (int64_t)j0 * L.vq_n, L.vs + (int64_t)j0 * L.vs_n,
+                               L.vz + (int64_t)j0 * L.vs_n, W.vo[i]);
+        }
+    } else if constexpr (KIND == 1) {
+        const int nv = min(UNIT, end - j0);   // tokens of the unit in the prefix
+#pragma unroll
+        for (int i = 0; i < SmallWords<D>::NI; ++i) {
+            const int t = (lane + 64 * i) / (D / 16);
+            const int shift = t < nv ? 0 : t - (nv - 1);   // clamp to the last token
+            const int64_t jt = (int64_t)(j0 - L.nq) - shift;
+            d32_load(W.k[i], L.kf + jt * L.kf_n * 2, W.ko[i].x);
+            if (value) d32_load(W.v[i], L.vf + jt * L.vf_n * 2, W.vo[i].x);
+        }
+    }
+}
+
+// the units [u0, u1) of this wave (unit u0 already loaded when `loaded`)
+template <int D, int KIND, int ROWS>
+__device__ __forceinline__ void small_units(const ScoreArgs &a, SmallSmem<D> &sm, const Lane &L, SmallWords<D> &W,
+                                            int bh, int wave, int u0, int u1, int end, bool loaded) {
+    constexpr int KS = D + 8, NI = SmallWords<D>::NI;
+    const int lane = threadIdx.x & 63;
+    uint16_t *Ks = sm.k[wave];
+    float *dist = sm.dist[wave];
+    const bool value = a.value;
+    const int vround = a.vround;
+    const float inv_r2 = 1.0f / (float)a.r2_total, sl2 = a.sl2;
+    if (!loaded) {
+        small_offsets<D, KIND>(L, W);
+        small_load<D, KIND>(L, W, u0, end, value);
+    }
+    for (int uu = u0; uu < u1; ++uu) {
+        const int j0 = uu * UNIT;
+        // ---- staging: K into the LDS tile, V distances per token
+        if constexpr (KIND == 2) {
+#pragma unroll 1
+            for (int i = 0; i < NI; ++i) {
+                const int u = lane + 64 * i, t = u / (D / 16), c0 = (u % (D / 16)) * 16;
+                const int j = min(j0 + t, end - 1);
+                uint32_t *dst = (uint32_t *)&Ks[t * KS + c0];
+#pragma unroll 4
+                for (int c = 0; c < 16; c += 2)
+                    dst[c / 2] = ma_pack_bf16x2(lane_key(L, j, c0 + c), lane_key(L, j, c0 + c + 1));
+                if (value) {
+                    float dd = vg_dist<D>(L, u, j0, end, &sm.cen[c0], vround);
+                    dd = token_sum<D>(dd);
+                    if (u % (D / 16) == 0) dist[t] = dd;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int u = lane + 64 * i;
+                if constexpr (KIND == 0) kp_store<D>(Ks, W.k[i], u);
+                else kd_store<D>(Ks, W.k[i], u, L.fdtype);
+                if (value) {
+                    const float *cen16 = &sm.cen[(u % (D / 16)) * 16];
+                    float dd;
+                    if constexpr (KIND == 0)
+                        dd = vround == MA_BF16 ? vp_dist<MA_BF16>(W.v[i], cen16)
+                                               : (vround == MA_F16 ? vp_dist<MA_F16>(W.v[i], cen16) : vp_dist<0>(W.v[i], cen16));
+                    else dd = vd_dist(W.v[i], cen16, L.fdtype);
+                    dd = token_sum<D>(dd);
+                    if (u % (D / 16) == 0) dist[u / (D / 16)] = dd;
+                }
+            }
+            if (uu + 1 < u1) small_load<D, KIND>(L, W, uu + 1, end, value);
+        }
+        wave_lds_sync();
+        // ---- scores: lane (token t, channel half hh)
+        const int t = lane & 31, hh = lane >> 5;
+        const uint4 *kr = (const uint4 *)&Ks[t * KS + hh * (D / 2)];
+        float acc[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            const uint4 kw = kr[c];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const uint4 qw = sm.qv[r][hh * (D / 16) + c];
+                float x = acc[r];
+                x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw.x), __builtin_bit_cast(bf16x2_t, kw.x), x, false);
+                x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw.y), __builtin_bit_cast(bf16x2_t, kw.y), x, false);
+                x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw.z), __builtin_bit_cast(bf16x2_t, kw.z), x, false);
+                x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw.w), __builtin_bit_cast(bf16x2_t, kw.w), x, false);
+                acc[r] = x;
+            }
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const float sv = ma_sum_xor32(acc[r]);   // both channel halves, the same in both lanes
+            m += __builtin_amdgcn_exp2f(__builtin_fmaf(sv, sl2, -sm.crow[r]));
+        }
+        const int j = j0 + t;
+        if (hh == 0 && j < end) {
+            const int64_t o = (int64_t)bh * end + j;
+            const bool live = !a.pre.mask || a.pre.mask[o] != 0;
+            const float mm = live ? m * inv_r2 : 0.f;
+            a.mass[o] = mm;
+            if (value) a.score[o] = live ? mm * __builtin_sqrtf(dist[t]) : 0.f;
+        }
+        // the next unit's staging overwrites this unit's LDS after these reads (in order)
+        wave_lds_sync();
+    }
+}
+
+template <int D, int ROWS>
+__global__ void __launch_bounds__(SM_NT) score_small_kernel(ScoreArgs a, int units, int dense_vec) {
+    __shared__ SmallSmem<D> sm;
+    const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int end = a.pre.nq + a.pre.nf;
+    const int R = a.R, R2 = a.R2, T = a.T, T2 = a.T2;
+    const bool ident = a.q_rows == nullptr;
+    // this wave's run of units: packed units [u0, pe) first, then the 16-bit tail [ts, u1)
+    const int w = blockIdx.x * SM_WAVES + wave;
+    const int u0 = w * a.per, u1 = min(units, u0 + a.per);
+    const Lane L = make_lane(a.pre, b, h, bh);
+    const int uq = L.nq / UNIT;
+    const int pe = min(u1, uq), ts = max(u0, uq);
+    const bool has_p = u0 < pe, has_t = ts < u1;
+    // the first unit's loads go out before the prologue's
+    SmallWords<D> W;
+    if (has_p) {
+        small_offsets<D, 0>(L, W);
+        small_load<D, 0>(L, W, u0, end, a.value);
+    } else if (has_t && dense_vec) {
+        small_offsets<D, 1>(L, W);
+        small_load<D, 1>(L, W, ts, end, a.value);
+    }
+    // ---- prologue: queries, row constants and the centre of the R2 <= ROWS rows
+    // selection row rr = g * T2 + i: block position t (clamped into the block), row g * T + t
+    auto sel = [&](int rr, int &g, int &t) {
+        g = rr / T2;
+        const int i = rr - g * T2;
+        t = min(max(ident ? a.row0 + i : a.q_rows[i], 0), T - 1);
+    };
+    for (int e = tid; e < ROWS * (D / 8); e += SM_NT) {
+        const int rr = e / (D / 8), c = e % (D / 8);
+        int g, t;
+        sel(rr < R2 ? rr : 0, g, t);
+        const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
+        const bf16x8_t x = ma_load8_as_bf16(a.q.ptr, qb + c * 8, a.q.dtype);
+        sm.qv[rr][c] = rr < R2 ? __builtin_bit_cast(uint4, x) : uint4{0u, 0u, 0u, 0u};
+    }
+    if (tid < ROWS) {
+        int g, t;
+        sel(tid < R2 ? tid : 0, g, t);
+        const float m = a.mp[(int64_t)bh * R + g * T + t], l = a.lp[(int64_t)bh * R + g * T + t];
+        sm.crow[tid] = tid < R2 && l > 0.f ? __builtin_fmaf(m, MA_LOG2E, __log2f(l)) : __builtin_inff();
+    }
+    if (a.value && tid < D) {
+        // all R2 loads in flight together (padding rows load row 0 and are not summed), then
+        // the sum in row order
+        float x[ROWS];
+#pragma unroll
+        for (int rr = 0; rr < ROWS; ++rr) {
+            int g, t;
+            sel(rr < R2 ? rr : 0, g, t);
+            const int64_t off = ((int64_t)bh * R + g * T + t) * D + tid;
+            if (a.op_dtype == MA_F32) x[rr] = ((const float *)a.op)[off];
+            else x[rr] = __uint_as_float((uint32_t)((const uint16_t *)a.op)[off]);   // raw bits, below
+        }
+        float c = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < ROWS; ++rr) {
+            if (rr < R2) {
+                const uint32_t bits = __float_as_uint(x[rr]);
+                c += a.op_dtype == MA_F32 ? x[rr] : a.op_dtype == MA_BF16 ? ma_bf16_to_f32((uint16_t)bits)
+                                                                           : ma_f16_to_f32((uint16_t)bits);
+            }
+        }
+        sm.cen[tid] = c / (float)R2;
+    }
+    __syncthreads();
+    if (has_p) small_units<D, 0, ROWS>(a, sm, L, W, bh, wave, u0, pe, end, true);
+    if (has_t) {
+        if (dense_vec) small_units<D, 1, ROWS>(a, sm, L, W, bh, wave, ts, u1, end, !has_p);
+        else small_units<D, 2, ROWS>(a, sm, L, W, bh, wave, ts, u1, end, false);
+    }
+}
+
 // the value centre of prefix_scores alone (same definition and order as score_kernel)
 template <int D>
 __global__ void __launch_bounds__(SNT) centre_kernel(const void *op, int op_dtype, int G, int T,
@@ -686,6 +953,18 @@ __global__ void __launch_bounds__(SNT) centre_kernel(const void *op, int op_dtyp
 }  // namespace
 
 int ma_validate_prefix(const ma_prefix *p, int D, const char *who);
+
+// 0: the VALU pass for at most AUTO_SMALL_ROWS selection rows, MFMA otherwise; 1: always
+// MFMA; 2: always VALU (calls with more than SMALL_ROWS rows fail)
+static std::atomic<int> g_score_path{0};
+
+extern "C" int ma_prefix_scores_path(int mode) {
+    if (mode < 0 || mode > 2) {
+        ma_set_error("ma_prefix_scores_path: mode must be 0 (auto), 1 (MFMA) or 2 (VALU)");
+        return -1;
+    }
+    return g_score_path.exchange(mode);
+}
 
 extern "C" int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, int D, const int32_t *q_rows,
                                int T2, float *centre, void *stream) {
@@ -771,7 +1050,7 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     int per = nfast > 0 ? (nfast * B * H + slots - 1) / slots : 1;
     if (per < 1) per = 1;
     const int fast_wgs = nfast > 0 ? (nfast + per - 1) / per : 0;
-    ScoreArgs sa;
+    ScoreArgs sa{};
     sa.q = q;
     sa.pre = prefix_dev(p);
     sa.q_rows = q_rows;
@@ -792,12 +1071,49 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
         return MA_EINVAL;
     }
     sa.vround = v_round;
+    sa.sl2 = scale * MA_LOG2E;
+    hipStream_t st = (hipStream_t)stream;
+    // at most SMALL_ROWS selection rows: the GQA-reduced VALU pass, one pass over the rows
+    const int path = g_score_path.load(std::memory_order_relaxed);
+    if (path == 2 && R2 > SMALL_ROWS) {
+        ma_set_error("%s: the VALU score pass takes at most %d selection rows per KV head, got %d", who, SMALL_ROWS,
+                     R2);
+        return MA_EUNSUPPORTED;
+    }
+    // (auto: up to AUTO_SMALL_ROWS rows, where it measured at least as fast as the padded
+    // MFMA pass at config 2's prefix; at 14 rows the dot products make it VALU-bound)
+    if (path == 2 || (path == 0 && R2 <= AUTO_SMALL_ROWS)) {
+        const int units = (n + UNIT - 1) / UNIT;
+        // about 8 waves per CU in all, each on a contiguous run of units
+        const int waves_bh = max(1, min(units, 8 * ma_num_cus() / (B * H)));
+        const int per = (units + waves_bh - 1) / waves_bh;
+        const int waves = (units + per - 1) / per;
+        sa.q_rows = q_rows;
+        sa.row0 = 0;
+        sa.T2 = T2;
+        sa.R2 = R2;
+        sa.row_tiles = 1;
+        sa.accum = 0;
+        sa.per = per;
+        const dim3 g2((waves + SM_WAVES - 1) / SM_WAVES, B * H);
+        const int dv = dense_vec_ok ? 1 : 0;
+#define MA_SMALL(D_, R_) hipLaunchKernelGGL((score_small_kernel<D_, R_>), g2, dim3(SM_NT), 0, st, sa, units, dv)
+        if (D == 128) {
+            if (R2 <= 4) MA_SMALL(128, 4);
+            else if (R2 <= 8) MA_SMALL(128, 8);
+            else MA_SMALL(128, 16);
+        } else {
+            if (R2 <= 4) MA_SMALL(64, 4);
+            else if (R2 <= 8) MA_SMALL(64, 8);
+            else MA_SMALL(64, 16);
+        }
+#undef MA_SMALL
+        return ma_check_launch(who);
+    }
     sa.nfast = nfast;
     sa.per = per;
     sa.fast_wgs = fast_wgs;
-    sa.sl2 = scale * MA_LOG2E;
     dim3 grid(fast_wgs + (tiles - nfast), B * H);
-    hipStream_t st = (hipStream_t)stream;
 #define MA_SCORE(D_, S_, H_) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT>), grid, dim3(SNT), 0, st, sa)
 #define MA_SCORE_I(D_, S_)                        \
     do {                                          \
