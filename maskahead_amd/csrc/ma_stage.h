@@ -52,7 +52,7 @@ struct StageShape {
     static constexpr int KPL = (NK + KLANES - 1) / KLANES;                   // items per K lane
     static constexpr int VPL = (NV + KLANES - 1) / KLANES;                   // items per V lane
     static constexpr int NWK = SRC == ST_PACKED ? 6 * KPL : 4 * KPL;
-    static constexpr int NWV = SRC == ST_PACKED ? 6 * VPL : 8 * VPL;
+    static constexpr int NWV = 8 * VPL;
     static constexpr int NW = NWK > NWV ? NWK : NWV;
 };
 
@@ -160,8 +160,10 @@ __device__ __forceinline__ void load_v_packed(uint32_t *w, uint32_t &flags, cons
     w[1] = l0 ? x0.y : 0u;
     w[2] = l1 ? x1.x : 0u;
     w[3] = l1 ? x1.y : 0u;
-    w[4] = (l0 ? s0 : 0u) | ((l1 ? s1 : 0u) << 16);
-    w[5] = (l0 ? z0 : 0u) | ((l1 ? z1 : 0u) << 16);
+    w[4] = l0 ? s0 : 0u;
+    w[5] = l1 ? s1 : 0u;
+    w[6] = l0 ? z0 : 0u;
+    w[7] = l1 ? z1 : 0u;
     flags = (l0 ? 1u : 0u) | (l1 ? 2u : 0u);
 }
 
@@ -171,25 +173,28 @@ __device__ __forceinline__ uint2 v_item_offsets(const Lane &L, int u) {
     const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
     return uint2{(uint32_t)(2 * tp * L.vq_n + cg * L.vq_c + ch * 8), (uint32_t)(2 * tp * L.vs_n + cg)};
 }
+// (every loaded value goes to a word of its own: combining the 16-bit scales here would
+// make the wave wait for the loads where they are issued, a tile ahead of their use)
 __device__ __forceinline__ void load_v_packed_fast(uint32_t *w, const uint8_t *vq, const uint16_t *vs,
                                                    const uint16_t *vz, int vq_n, int vs_n, uint2 o) {
     const uint2 x0 = *(const uint2 *)(vq + o.x);
     const uint2 x1 = *(const uint2 *)(vq + o.x + vq_n);
-    const uint32_t s0 = vs[o.y], z0 = vz[o.y], s1 = vs[o.y + vs_n], z1 = vz[o.y + vs_n];
     w[0] = x0.x;
     w[1] = x0.y;
     w[2] = x1.x;
     w[3] = x1.y;
-    w[4] = s0 | (s1 << 16);
-    w[5] = z0 | (z1 << 16);
+    w[4] = vs[o.y];
+    w[5] = vs[o.y + vs_n];
+    w[6] = vz[o.y];
+    w[7] = vz[o.y + vs_n];
 }
 
 template <int D>
 __device__ __forceinline__ void store_v_packed(uint16_t *Vt, const uint32_t *w, int u) {
     constexpr int VS = TILE + 8;
     const int tp = u & 31, ch = (u >> 5) & 1, cg = u >> 6;
-    const float s0 = ma_f16_to_f32(w[4] & 0xffff), s1 = ma_f16_to_f32(w[4] >> 16);
-    const float z0 = ma_f16_to_f32(w[5] & 0xffff), z1 = ma_f16_to_f32(w[5] >> 16);
+    const float s0 = ma_f16_to_f32((uint16_t)w[4]), s1 = ma_f16_to_f32((uint16_t)w[5]);
+    const float z0 = ma_f16_to_f32((uint16_t)w[6]), z1 = ma_f16_to_f32((uint16_t)w[7]);
     uint32_t *dst = (uint32_t *)&Vt[(cg * VGRP + ch * 16) * VS + vcol(2 * tp)];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {   // code word q: channels 8q .. 8q+7 of the half
