@@ -9,9 +9,9 @@
 //   goes through f32 first, which is how a float64 value becomes bfloat16 in torch.
 //   fp32 mode (the reference's BITSIEVE_VSCORE_FP32 branch): the same formula in f32 on
 //   the stored values, sums in f64.
-//   Three launches: per-chunk partial sums (grid chunks x rows), the centre per row, the
-//   per-entry distances and scores (grid chunks x rows).  Fixed summation order: results
-//   are deterministic.
+//   Three launches: per-chunk partial sums (grid chunks x rows, chunks of 256 entries),
+//   the centre per row, the per-entry distances and scores (grid chunks x rows).  Fixed
+//   summation order: results are deterministic.
 //
 // compaction (cache.py:342-367 / 659-678, eviction.py:411-418): dst[i] = src[keep[i]] for
 //   i < C, in place, for several token-major planes of one lane at once (bf16 K and V,
@@ -29,6 +29,8 @@ namespace {
 
 constexpr int VS_TOK = 16;   // tokens per step of a 256-thread value-score workgroup
 constexpr int VS_NT = 256;
+constexpr int VS_CHUNK = 256;   // tokens per workgroup: 16 steps, loaded VS_BATCH steps at a time
+constexpr int VS_BATCH = 4;
 
 // f64 -> bf16 the way torch converts a float64 tensor: to f32 (nearest even), then to bf16
 // (nearest even).  The second rounding is done on the f32 bits with integer arithmetic so
@@ -91,16 +93,28 @@ __global__ void __launch_bounds__(VS_NT) vs_partial_kernel(VsArgs a) {
     const float *ar = a.a + (int64_t)row * a.sa;
     double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     double den = 0.0;
-    for (int j = j0 + tl; j < j1; j += VS_TOK) {
-        const float aj = ar[j];
-        const double w = a.fp32_mode ? (double)aj : (double)ma_round_bf16(aj);
-        if (cok) {
-            float x[8];
-            load8(vrow(a, row, j), c0, a.vdtype, x);
+    // VS_BATCH steps' loads in flight together (tokens past the chunk load the chunk's first
+    // token and weigh 0); the f64 sums of these products are exact, so the order of the
+    // steps does not change the result
+    for (int jb = j0; jb < j1; jb += VS_TOK * VS_BATCH) {
+        float aw[VS_BATCH], x[VS_BATCH][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = __builtin_fma(w, (double)x[i], acc[i]);
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const int j = jb + u * VS_TOK + tl;
+            const bool ok = j < j1;
+            const int jl = ok ? j : j0;
+            aw[u] = ok ? ar[jl] : 0.f;
+            if (cok) load8(vrow(a, row, jl), c0, a.vdtype, x[u]);
         }
-        den += w;
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const double w = a.fp32_mode ? (double)aw[u] : (double)ma_round_bf16(aw[u]);
+            if (cok) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[i] = __builtin_fma(w, (double)x[u][i], acc[i]);
+            }
+            den += w;
+        }
     }
     if (cok)
 #pragma unroll
@@ -124,12 +138,14 @@ __global__ void __launch_bounds__(128) vs_centre_kernel(VsArgs a) {
     const double *p = a.part + (int64_t)row * a.nchunks * (a.D + 1);
     if (d == 0) {
         double den = 0.0;
+#pragma unroll 8
         for (int c = 0; c < a.nchunks; ++c) den += p[(int64_t)c * (a.D + 1) + a.D];
         s_den = den;
     }
     __syncthreads();
     if (d >= a.D) return;
     double num = 0.0;
+#pragma unroll 8
     for (int c = 0; c < a.nchunks; ++c) num += p[(int64_t)c * (a.D + 1) + d];
     float cen;
     if (a.fp32_mode) {
@@ -158,29 +174,40 @@ __global__ void __launch_bounds__(VS_NT) vs_score_kernel(VsArgs a) {
     const int j0 = chunk * a.chunk, j1 = min(j0 + a.chunk, a.n);
     const float *ar = a.a + (int64_t)row * a.sa;
     float *sr = a.score + (int64_t)row * a.ss;
-    for (int jb = j0; jb < j1; jb += VS_TOK) {
-        const int j = jb + tl;
-        const bool ok = j < j1;
-        double ss = 0.0;
-        if (ok && cok) {
-            float x[8];
-            load8(vrow(a, row, j), c0, a.vdtype, x);
+    float cc[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float dl = x[i] - cen[c0 + i];          // exact difference rounded to f32
-                if (!a.fp32_mode) dl = ma_round_bf16(dl);
-                ss = __builtin_fma((double)dl, (double)dl, ss);
-            }
+    for (int i = 0; i < 8; ++i) cc[i] = cok ? cen[c0 + i] : 0.f;
+    for (int jb0 = j0; jb0 < j1; jb0 += VS_TOK * VS_BATCH) {
+        // VS_BATCH steps' loads in flight together (tokens past the chunk are not written)
+        float x[VS_BATCH][8], aw[VS_BATCH];
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const int j = jb0 + u * VS_TOK + tl;
+            const int jl = j < j1 ? j : j0;
+            if (cok) load8(vrow(a, row, jl), c0, a.vdtype, x[u]);
+            aw[u] = ar[jl];
         }
-        // sum over the 16 lanes of this entry (lanes tl*16 .. tl*16+15 of the wave pair)
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
-        if (ok && oc == 0) {
-            const float aj = ar[j];
-            float nrm;
-            if (a.fp32_mode) nrm = (float)__builtin_sqrt(ss);
-            else nrm = bf16_via_f32(__builtin_sqrt(ss));
-            sr[j] = aj * nrm;
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const int j = jb0 + u * VS_TOK + tl;
+            double ss = 0.0;
+            if (cok) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    float dl = x[u][i] - cc[i];          // exact difference rounded to f32
+                    if (!a.fp32_mode) dl = ma_round_bf16(dl);
+                    ss = __builtin_fma((double)dl, (double)dl, ss);
+                }
+            }
+            // sum over the 16 lanes of this entry (lanes tl*16 .. tl*16+15 of the wave pair)
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+            if (j < j1 && oc == 0) {
+                float nrm;
+                if (a.fp32_mode) nrm = (float)__builtin_sqrt(ss);
+                else nrm = bf16_via_f32(__builtin_sqrt(ss));
+                sr[j] = aw[u] * nrm;
+            }
         }
     }
 }
@@ -285,8 +312,7 @@ __global__ void __launch_bounds__(256) append_kernel(ma_tensor4 src, ma_tensor4 
 
 extern "C" int64_t ma_value_score_workspace_bytes(int rows, int n, int D) {
     if (rows <= 0 || n < 0 || D <= 0 || D > 128) return -1;
-    const int chunk = 2048;
-    const int nchunks = n ? (n + chunk - 1) / chunk : 1;
+    const int nchunks = n ? (n + VS_CHUNK - 1) / VS_CHUNK : 1;
     return (int64_t)rows * nchunks * (D + 1) * 8 + (int64_t)rows * D * 4 + 256;
 }
 
@@ -323,7 +349,7 @@ extern "C" int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, in
     va.D = D;
     va.vdtype = v.dtype;
     va.fp32_mode = fp32_mode;
-    va.chunk = 2048;
+    va.chunk = VS_CHUNK;
     va.nchunks = (n + va.chunk - 1) / va.chunk;
     va.part = (double *)(((uintptr_t)workspace + 15) & ~(uintptr_t)15);
     va.centre = (float *)(va.part + (int64_t)rows * va.nchunks * (D + 1));

@@ -333,14 +333,14 @@ __device__ __forceinline__ void cur_segment(const FwdArgs &a, const Work &wk, Fw
             uint32_t w[8];
             const char *kb = kc.base + (int64_t)n0 * kc.sn * kc.esz;
             for (int u = sl; u < TILE * D / 8; u += nsl) {
-                load_k_dense<D>(w, kb, kc.sn, kc.dtype, kc.esz, u, valid);
-                store_k_dense<D>(S.kt[0].k, w, u);
+                const bool ok = load_k_dense<D>(w, kb, kc.sn, kc.dtype, kc.esz, u, valid);
+                store_k_dense<D>(S.kt[0].k, w, u, kc.dtype, ok);
             }
             const char *vb = vc.base + (int64_t)n0 * vc.sn * vc.esz;
             for (int u = sl; u < TILE / 2 * D / 8; u += nsl) {
                 const int tp = u % (TILE / 2);
-                load_v_dense<D>(w, vb, vc.sn, vc.dtype, vc.esz, u, 2 * tp < valid, 2 * tp + 1 < valid, valid);
-                store_v_dense<D>(S.vt[0].vt, w, u);
+                load_v_dense<D>(w, vb, vc.sn, vc.dtype, vc.esz, u, valid);
+                store_v_dense<D>(S.vt[0].vt, w, u, vc.dtype, 2 * tp < valid, 2 * tp + 1 < valid);
             }
             if (wave == 7) {
                 const uint64_t m = __ballot(lane < valid);
@@ -458,7 +458,8 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
 #pragma unroll
             for (int r = 0; r < Shape::KPL; ++r) {
                 const int u = kl + r * KLANES;
-                if (u < Shape::NK) load_k_dense<D>(&pr.w[4 * r], base, ds.sk, ds.dtype, ds.esz, u, n_end - n0);
+                if (u < Shape::NK && load_k_dense<D>(&pr.w[4 * r], base, ds.sk, ds.dtype, ds.esz, u, n_end - n0))
+                    pr.flags |= 1u << r;   // bit r: item r's token below the end
             }
         }
     };
@@ -470,7 +471,7 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
 #pragma unroll
             for (int r = 0; r < Shape::KPL; ++r) {
                 const int u = kl + r * KLANES;
-                if (u < Shape::NK) store_k_dense<D>(Ks, &pr.w[4 * r], u);
+                if (u < Shape::NK) store_k_dense<D>(Ks, &pr.w[4 * r], u, ds.dtype, (pr.flags >> r) & 1u);
             }
         }
         if (kl < TILE) {
@@ -495,13 +496,15 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             if (vl < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vl, n0, n_end);
         } else {
             const char *base = ds.v + (int64_t)(n0 - ds.tok0) * ds.sv * ds.esz;
+            pr.flags = 0u;   // bits 2r, 2r+1: item r's two tokens live
 #pragma unroll
             for (int r = 0; r < Shape::VPL; ++r) {
                 const int u = vl + r * KLANES;
                 if (u < Shape::NV) {
                     const int tp = u % (TILE / 2);
-                    load_v_dense<D>(&pr.w[8 * r], base, ds.sv, ds.dtype, ds.esz, u, live(n0 + 2 * tp),
-                                    live(n0 + 2 * tp + 1), n_end - n0);
+                    load_v_dense<D>(&pr.w[8 * r], base, ds.sv, ds.dtype, ds.esz, u, n_end - n0);
+                    pr.flags |= (live(n0 + 2 * tp) ? 1u : 0u) << (2 * r);
+                    pr.flags |= (live(n0 + 2 * tp + 1) ? 1u : 0u) << (2 * r + 1);
                 }
             }
         }
@@ -514,7 +517,9 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
 #pragma unroll
             for (int r = 0; r < Shape::VPL; ++r) {
                 const int u = vl + r * KLANES;
-                if (u < Shape::NV) store_v_dense<D>(Vt, &pr.w[8 * r], u);
+                if (u < Shape::NV)
+                    store_v_dense<D>(Vt, &pr.w[8 * r], u, ds.dtype, (pr.flags >> (2 * r)) & 1u,
+                                     (pr.flags >> (2 * r + 1)) & 1u);
             }
         }
     };

@@ -207,39 +207,56 @@ __device__ __forceinline__ void store_v_packed(uint16_t *Vt, const uint32_t *w, 
 
 // ------------------------------------------------------------------ 16/32-bit K and V
 // base: byte pointer of token 0 of the tile; sn: elements per token; tokens usable below
-// `valid` (relative); dead tokens (live == false) are zeroed by the caller for V.
+// `valid` (relative).  The loads keep bf16 and f16 words as stored (token indices clamped
+// into the tile, so every load is valid); the conversion to bf16 and the zeroing of
+// unusable or dead tokens happen when the words are staged, so the loads of a prefetched
+// tile are not waited on where they are issued.  f32 sources are converted at load.
+__device__ __forceinline__ uint4 load8_raw(const char *p, int dtype) {
+    if (dtype == MA_F32) return __builtin_bit_cast(uint4, ma_load8_as_bf16(p, 0, MA_F32));
+    return *(const uint4 *)p;
+}
+// the 8 elements of a raw item as bf16 pairs, zero when !ok
+__device__ __forceinline__ uint4 stage8(uint4 w, int dtype, bool ok) {
+    if (!ok) return uint4{0u, 0u, 0u, 0u};
+    if (dtype == MA_F16) {   // f16 keys and values enter the MFMAs as bf16 (splitk.py:139, 152)
+        const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = ma_pack_bf16x2(ma_f16_to_f32(x[e] & 0xffff), ma_f16_to_f32(x[e] >> 16));
+        return uint4{o[0], o[1], o[2], o[3]};
+    }
+    return w;
+}
+
+// item u of a K tile: token u / (D/8), 8 channels; returns whether the token is below `valid`
 template <int D>
-__device__ __forceinline__ void load_k_dense(uint32_t *w, const char *base, int sn, int dtype, int esz, int u,
+__device__ __forceinline__ bool load_k_dense(uint32_t *w, const char *base, int sn, int dtype, int esz, int u,
                                              int valid) {
     const int t = u / (D / 8), chk = u % (D / 8);
     const int tc = min(t, valid - 1);
-    bf16x8_t x = load8_bf16(base + ((int64_t)tc * sn + chk * 8) * esz, dtype);
-    if (t >= valid) x = bf16x8_t{};
-    const uint4 q = __builtin_bit_cast(uint4, x);
+    const uint4 q = load8_raw(base + ((int64_t)tc * sn + chk * 8) * esz, dtype);
     w[0] = q.x;
     w[1] = q.y;
     w[2] = q.z;
     w[3] = q.w;
+    return t < valid;
 }
 
 template <int D>
-__device__ __forceinline__ void store_k_dense(uint16_t *Ks, const uint32_t *w, int u) {
+__device__ __forceinline__ void store_k_dense(uint16_t *Ks, const uint32_t *w, int u, int dtype, bool ok) {
     constexpr int KS = D + 8;
     const int t = u / (D / 8), chk = u % (D / 8);
-    *(uint4 *)&Ks[t * KS + chk * 8] = uint4{w[0], w[1], w[2], w[3]};
+    *(uint4 *)&Ks[t * KS + chk * 8] = stage8(uint4{w[0], w[1], w[2], w[3]}, dtype, ok);
 }
 
-// item u: tp = u % 32, chk = u / 32
+// item u of a V tile: tokens 2tp, 2tp+1 (tp = u % 32), 8 channels (chunk u / 32)
 template <int D>
 __device__ __forceinline__ void load_v_dense(uint32_t *w, const char *base, int sn, int dtype, int esz, int u,
-                                             bool l0, bool l1, int valid) {
+                                             int valid) {
     const int tp = u % (TILE / 2), chk = u / (TILE / 2);
     const int t0 = min(2 * tp, valid - 1), t1 = min(2 * tp + 1, valid - 1);
-    bf16x8_t x0 = load8_bf16(base + ((int64_t)t0 * sn + chk * 8) * esz, dtype);
-    bf16x8_t x1 = load8_bf16(base + ((int64_t)t1 * sn + chk * 8) * esz, dtype);
-    if (!l0) x0 = bf16x8_t{};
-    if (!l1) x1 = bf16x8_t{};
-    const uint4 a = __builtin_bit_cast(uint4, x0), b = __builtin_bit_cast(uint4, x1);
+    const uint4 a = load8_raw(base + ((int64_t)t0 * sn + chk * 8) * esz, dtype);
+    const uint4 b = load8_raw(base + ((int64_t)t1 * sn + chk * 8) * esz, dtype);
     w[0] = a.x;
     w[1] = a.y;
     w[2] = a.z;
@@ -250,15 +267,19 @@ __device__ __forceinline__ void load_v_dense(uint32_t *w, const char *base, int 
     w[7] = b.w;
 }
 
+// l0, l1: the two tokens are live (dead ones are staged as zeros)
 template <int D>
-__device__ __forceinline__ void store_v_dense(uint16_t *Vt, const uint32_t *w, int u) {
+__device__ __forceinline__ void store_v_dense(uint16_t *Vt, const uint32_t *w, int u, int dtype, bool l0, bool l1) {
     constexpr int VS = TILE + 8;
     const int tp = u % (TILE / 2), chk = u / (TILE / 2);
     const int col = vcol(2 * tp);
+    const uint4 a = stage8(uint4{w[0], w[1], w[2], w[3]}, dtype, l0);
+    const uint4 b = stage8(uint4{w[4], w[5], w[6], w[7]}, dtype, l1);
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (w[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const uint32_t hi = (w[4 + (e >> 1)] >> ((e & 1) * 16)) & 0xffffu;
+        const uint32_t lo = (wa[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        const uint32_t hi = (wb[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
         *(uint32_t *)&Vt[(chk * 8 + e) * VS + col] = lo | (hi << 16);
     }
 }
