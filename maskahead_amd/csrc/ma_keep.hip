@@ -131,34 +131,50 @@ __global__ void __launch_bounds__(VS_NT) vs_partial_kernel(VsArgs a) {
     }
 }
 
-// grid rows, 128 threads: centre[row, d] from the chunk partials (fixed order)
-__global__ void __launch_bounds__(128) vs_centre_kernel(VsArgs a) {
-    __shared__ double s_den;
-    const int row = blockIdx.x, d = threadIdx.x;
+// grid rows, VC_NT threads: centre[row, d] from the chunk partials.  Thread (slot s,
+// column d) sums the chunks s, s + VC_SLOTS, ... (VC_UNROLL loads in flight), then the
+// slots are added in slot order: a fixed order, and in the bf16 mode every sum of the
+// products is exact in f64, so no order changes a result there.
+constexpr int VC_SLOTS = 8, VC_NT = 1024, VC_UNROLL = 8;
+__global__ void __launch_bounds__(VC_NT) vs_centre_kernel(VsArgs a) {
+    __shared__ double part[VC_SLOTS][129];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int slot = tid / 128, d = tid % 128;   // column D is the denominator
     const double *p = a.part + (int64_t)row * a.nchunks * (a.D + 1);
-    if (d == 0) {
-        double den = 0.0;
-#pragma unroll 8
-        for (int c = 0; c < a.nchunks; ++c) den += p[(int64_t)c * (a.D + 1) + a.D];
-        s_den = den;
+    if (d <= a.D) {
+        double acc = 0.0;
+#pragma unroll VC_UNROLL
+        for (int c = slot; c < a.nchunks; c += VC_SLOTS) acc += p[(int64_t)c * (a.D + 1) + d];
+        part[slot][d] = acc;
+    }
+    // with D == 128 the denominator column has no thread of its own: column 0's threads of
+    // every slot sum it as well
+    if (a.D == 128 && d == 0) {
+        double acc = 0.0;
+#pragma unroll VC_UNROLL
+        for (int c = slot; c < a.nchunks; c += VC_SLOTS) acc += p[(int64_t)c * (a.D + 1) + 128];
+        part[slot][128] = acc;
     }
     __syncthreads();
-    if (d >= a.D) return;
-    double num = 0.0;
-#pragma unroll 8
-    for (int c = 0; c < a.nchunks; ++c) num += p[(int64_t)c * (a.D + 1) + d];
+    if (tid >= a.D) return;
+    double num = 0.0, den = 0.0;
+#pragma unroll
+    for (int s2 = 0; s2 < VC_SLOTS; ++s2) {
+        num += part[s2][tid];
+        den += part[s2][a.D];
+    }
     float cen;
     if (a.fp32_mode) {
-        const double den = s_den > 1e-12 ? s_den : 1e-12;
-        cen = (float)(num / den);
+        const double dd = den > 1e-12 ? den : 1e-12;
+        cen = (float)(num / dd);
     } else {
         const double nb = (double)bf16_via_f32(num);
-        double db = (double)bf16_via_f32(s_den);
+        double db = (double)bf16_via_f32(den);
         const double lo = (double)bf16_via_f32(1e-12);
         if (!(db >= lo)) db = lo;   // torch.clamp_min on the bf16 sum
         cen = bf16_via_f32(nb / db);
     }
-    a.centre[(int64_t)row * a.D + d] = cen;
+    a.centre[(int64_t)row * a.D + tid] = cen;
 }
 
 // grid (nchunks, rows), 256 threads: one 16-channel slice of one entry per thread pair...
@@ -358,7 +374,7 @@ extern "C" int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, in
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid(va.nchunks, rows);
     hipLaunchKernelGGL(vs_partial_kernel, grid, dim3(VS_NT), 0, st, va);
-    hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(128), 0, st, va);
+    hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
     hipLaunchKernelGGL(vs_score_kernel, grid, dim3(VS_NT), 0, st, va);
     return ma_check_launch(who);
 }
