@@ -46,6 +46,9 @@ constexpr int H1 = 1 << D1_BITS;        // 2048 level-1 bins
 constexpr int H2 = 1 << D2_BITS;        // 256 level-2 bins
 constexpr int MAX_CHUNKS = 1024;        // per row (4 chunks per thread in the chunk scans)
 constexpr int NCR = 8;                  // candidates per thread kept in registers by the emit kernel
+constexpr int NCL = 8192;               // candidates per row kept in LDS beyond that (a boundary bin
+                                        // of a value-aware keep contest at 64k entries holds a few
+                                        // thousand); more are re-read from the workspace
 static_assert(D0_BITS + D1_BITS + D2_BITS == 32, "digits cover the key");
 
 // one row's block of the state buffer
@@ -294,7 +297,10 @@ struct EmitSmem {
     uint32_t ecnt[MAX_CHUNKS];      // per chunk: candidates equal to T
     uint32_t wsum[4 * TW], found[2];   // (block_prefix_runs<NR> uses NR * TW)
     uint32_t base, take, eq;        // this workgroup's chunk
+    uint32_t ckey[NCL];             // the row's candidates (key, chunk) when more than
+    uint16_t cchk[NCL];             // fit in registers
 };
+static_assert(MAX_CHUNKS <= 65536, "chunk ids are 16-bit");
 
 // T, need and the chunk's base from the row's candidates; the chunk's selected indices,
 // ascending, to idx[base ..]; values optional.
@@ -363,7 +369,30 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
         return lo;
     };
     const bool inreg = NC <= (uint32_t)(NCR * TB);
+    const bool inlds = !inreg && NC <= (uint32_t)NCL;
     uint32_t ck[NCR], cc[NCR];
+    if (inlds) {
+        // batches of 8 candidates per thread, their loads in flight together
+        for (uint32_t g0 = 0; g0 < NC; g0 += 8 * TB) {
+            uint32_t kx[8];
+            int chs[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t g = g0 + tid + i * TB;
+                chs[i] = g < NC ? locate(g) : 0;
+                kx[i] = g < NC ? L[(int64_t)chs[i] * CS + (g - S.pre[chs[i]])].x : 0u;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t g = g0 + tid + i * TB;
+                if (g < NC) {
+                    S.ckey[g] = kx[i];
+                    S.cchk[g] = (uint16_t)chs[i];
+                }
+            }
+        }
+        __syncthreads();
+    }
     if (inreg) {
 #pragma unroll
         for (int i = 0; i < NCR; ++i) {
@@ -382,6 +411,8 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
 #pragma unroll
             for (int i = 0; i < NCR; ++i)
                 if (ck[i]) f(ck[i], cc[i]);
+        } else if (inlds) {
+            for (uint32_t g = tid; g < NC; g += TB) f(S.ckey[g], (uint32_t)S.cchk[g]);
         } else {
             for (uint32_t g = tid; g < NC; g += TB) {
                 const int ch = locate(g);
