@@ -8,6 +8,7 @@ kernel is not built for the requested shape, the call raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from pathlib import Path
 
@@ -112,6 +113,14 @@ def load(path: Path | str | None = None):
     return lib
 
 
+@functools.lru_cache(maxsize=4096)
+def size_query(name: str, *args) -> int:
+    """A workspace / state size entry point of the library (a pure function of its integer
+    arguments and of the device's CU count), memoized: the host path calls them on every
+    kernel call."""
+    return int(getattr(load(), name)(*args))
+
+
 def check(rc: int, what: str) -> None:
     if rc == MA_OK:
         return
@@ -155,13 +164,14 @@ def t4(t: torch.Tensor | None) -> MaTensor4:
     m = MaTensor4()
     if t is None:
         return m
-    if t.ndim != 4:
+    s = t.stride()
+    if len(s) != 4:
         raise ValueError(f"expected a 4-d tensor, got shape {tuple(t.shape)}")
-    if t.shape[-1] > 1 and t.stride(-1) != 1:
+    if s[3] != 1 and t.shape[3] > 1:
         raise ValueError("the innermost dimension must be contiguous")
     m.ptr = t.data_ptr()
     m.dtype = dtype_code(t.dtype)
-    m.s[0], m.s[1], m.s[2] = t.stride(0), t.stride(1), t.stride(2)
+    m.s[0], m.s[1], m.s[2] = s[0], s[1], s[2]
     return m
 
 

@@ -67,10 +67,10 @@ def keep_select(pos: torch.Tensor, score: torch.Tensor, capacity: int, window: i
         else:
             lo = int(lo)
     lib = N.load()
-    ws_bytes = int(lib.ma_topk_workspace_bytes(rows, n))
+    ws_bytes = N.size_query("ma_topk_workspace_bytes", rows, n)
     if ws_bytes <= 0:
         raise N.KernelUnavailableError(f"ma_keep_select: n={n} exceeds the built maximum")
-    st = select_state(score.device, int(lib.ma_topk_state_bytes(rows)))
+    st = select_state(score.device, N.size_query("ma_topk_state_bytes", rows))
     ws = torch.empty((ws_bytes,), device=score.device, dtype=torch.uint8)
     rc = lib.ma_keep_select(p2.data_ptr(), 1 if p2.dtype == torch.int64 else 0, p2.stride(0) if rows > 1 else n,
                             s2.data_ptr(), s2.stride(0) if rows > 1 else n, rows, n, capacity, int(window),

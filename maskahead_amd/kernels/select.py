@@ -21,9 +21,10 @@ from .. import _native as N
 _STATES: dict = {}
 
 
-def _state(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The zero-initialised select state of (`device`, its current stream), at least nbytes."""
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+def _state(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
+    """The zero-initialised select state of (`device`, its current stream -- `stream` when
+    the caller has it), at least nbytes."""
+    key = (device.index, stream if stream is not None else torch.cuda.current_stream(device).cuda_stream)
     st = _STATES.get(key)
     if st is None or st.numel() < nbytes:
         # allocated and zero-filled on the current stream; the old one goes back to the
@@ -69,11 +70,11 @@ def topk_ascending(rank: torch.Tensor, k: int, mask: torch.Tensor | None = None,
     if values is not None and (not values.is_contiguous() or values.numel() != rows * k):
         raise ValueError("values must be a contiguous f32 [..., k] tensor")
     lib = N.load()
-    ws_bytes = int(lib.ma_topk_workspace_bytes(rows, n))
+    ws_bytes = N.size_query("ma_topk_workspace_bytes", rows, n)
     if ws_bytes <= 0:
         raise N.KernelUnavailableError(f"ma_topk_select: n={n} exceeds the built maximum")
     stream = N.stream_of(rank)
-    st = state if state is not None else _state(rank.device, int(lib.ma_topk_state_bytes(rows)))
+    st = state if state is not None else _state(rank.device, N.size_query("ma_topk_state_bytes", rows), stream)
     ws = torch.empty((ws_bytes,), device=rank.device, dtype=torch.uint8)
     rc = lib.ma_topk_select(r2.data_ptr(), r2.stride(0) if rows > 1 else n, N.ptr(m2),
                             (m2.stride(0) if rows > 1 else n) if m2 is not None else 0, rows, n, k,
