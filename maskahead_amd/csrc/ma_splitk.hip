@@ -412,7 +412,10 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     // their registers for two tiles of S^T and the Q fragments
     const int st_lane = wave >= 7 ? tid - 7 * 64 : -1;
     const bool is_k = st_lane >= 0 && st_lane < KLANES;
-    const bool is_v = st_lane >= KLANES && st_lane < NSTAGE;
+    // packed: the V lanes of wave 11 (SIMD 3) stage here; those of waves 12..14 are taken
+    // by wave 15 (also SIMD 3, three items per lane), so the three SIMDs that carry two S
+    // and two O waves do no V staging (a SIMD's full-rate VALU and MFMA time add up)
+    const bool is_v = st_lane >= KLANES && st_lane < (SRC == 0 ? KLANES + 64 : NSTAGE);
     const int kl = st_lane, vl = st_lane - KLANES;
 
     auto tile_n0 = [&](int i) { return n_beg + i * TILE; };
@@ -482,18 +485,23 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     auto store_k = [&](uint16_t *Ks, uint64_t &km) { store_k_from(pr, Ks, km); };
     // V lanes: global loads of tile i into pr (or another register set); the dequant /
     // copy into a V buffer
+    // packed V item vx (offsets ox from the tile start) of tile i into pr
+    auto load_vp_item = [&](StageRegs<Shape::NW> &pr, int i, int vx, uint2 ox) {
+        const int n0 = tile_n0(i);
+        if (fast_tiles && n0 + TILE <= n_end) {
+            if (vx < Shape::NV) {
+                load_v_packed_fast(pr.w, L.vq + (int64_t)n0 * L.vq_n, L.vs + (int64_t)n0 * L.vs_n,
+                                   L.vz + (int64_t)n0 * L.vs_n, L.vq_n, L.vs_n, ox);
+                pr.flags = 3u;
+            }
+            return;
+        }
+        if (vx < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vx, n0, n_end);
+    };
     auto load_v_into = [&](StageRegs<Shape::NW> &pr, int i) {
         const int n0 = tile_n0(i);
         if constexpr (SRC == 0) {
-            if (fast_tiles && n0 + TILE <= n_end) {
-                if (vl < Shape::NV) {
-                    load_v_packed_fast(pr.w, L.vq + (int64_t)n0 * L.vq_n, L.vs + (int64_t)n0 * L.vs_n,
-                                       L.vz + (int64_t)n0 * L.vs_n, L.vq_n, L.vs_n, item_off);
-                    pr.flags = 3u;
-                }
-                return;
-            }
-            if (vl < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vl, n0, n_end);
+            load_vp_item(pr, i, vl, item_off);
         } else {
             const char *base = ds.v + (int64_t)(n0 - ds.tok0) * ds.sv * ds.esz;
             pr.flags = 0u;   // bits 2r, 2r+1: item r's two tokens live
@@ -583,6 +591,39 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             S.fin[rw][2][c32] = l;
         }
         __syncthreads();
+    } else if (SRC == 0 && wave == NTH / 64 - 1) {
+        // ---- packed V staging of V lanes 64 .. 255 (three items per lane): tile it in
+        // iteration it, the loads of tile it+1 behind it; the same barriers as the O waves
+        constexpr int NX = 3;
+        StageRegs<Shape::NW> vr[NX];
+        uint2 vo[NX];
+        int vx[NX];
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            vx[j] = 64 * (j + 1) + lane;
+            vr[j].flags = 0;
+            vo[j] = vx[j] < Shape::NV ? v_item_offsets<D>(L, vx[j]) : uint2{0u, 0u};
+        }
+        if (nt > 0) {
+#pragma unroll
+            for (int j = 0; j < NX; ++j) load_vp_item(vr[j], 0, vx[j], vo[j]);
+        }
+        __syncthreads();
+        __syncthreads();
+        for (int it = 0; it <= nt; ++it) {
+            if (it < nt) {
+                uint16_t *Vt = S.vt[it & 1].vt;
+#pragma unroll
+                for (int j = 0; j < NX; ++j)
+                    if (vx[j] < Shape::NV) store_v_packed<D>(Vt, vr[j].w, vx[j]);
+                if (it + 1 < nt) {
+#pragma unroll
+                    for (int j = 0; j < NX; ++j) load_vp_item(vr[j], it + 1, vx[j], vo[j]);
+                }
+            }
+            __syncthreads();
+        }
+        __syncthreads();  // final statistics of the S waves
     } else {
         // ---- O waves (PV one tile behind the S waves) and staging: K lanes stage tile it+2,
         // V lanes tile it
