@@ -352,6 +352,13 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
 
     // ---- fast staging state: this thread's item offsets inside a tile, once
     const int ni = value ? 2 * NIK : NIK;              // staging items per tile
+    // Thread t stages item (t + j NT + rot) mod (IPT NT).  When the K and V items fill the
+    // threads exactly, rot = NIK puts the V items (the dearer ones: dequantization plus the
+    // distance) on waves 0 .. NWV/2 - 1, whose S units come first in each SIMD's MFMA
+    // order, and the K items on the later waves, so that no wave has both the latest S
+    // unit and a V item.
+    const int rot = (value && 2 * NIK == IPT * NT) ? NIK : 0;
+    auto item = [&](int j) { return (tid + j * NT + rot) % (IPT * NT); };
     uint32_t w[IPT][NW];
     uint2 off[IPT];
 #pragma unroll
@@ -365,7 +372,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         const Lane L = make_lane(a.pre, b, h, bh);
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const int u = tid + j * NT;
+            const int u = item(j);
             if (u < NIK) off[j] = SRC == SRC_PACKED ? kp_offsets<D>(L, u) : uint2{kd_offset<D>(L, u), 0u};
             else if (u < ni)
                 off[j] = SRC == SRC_PACKED ? vp_offsets<D>(L, u - NIK) : uint2{vd_offset<D>(L, u - NIK), 0u};
@@ -391,7 +398,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         const int64_t ti = tile0 + i;   // whole tiles: packed tile ti starts at key group 2*ti
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const int u = tid + j * NT;
+            const int u = item(j);
             if (u < NIK) {
                 if constexpr (SRC == SRC_PACKED)
                     kp_load(w[j], kq0 + ti * kq_tile, ks0 + ti * ks_tile, kz0 + ti * ks_tile, kq_d, off[j]);
@@ -575,7 +582,13 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         if (j < end) {
             float s = 0.f;
             const int th = lane >> 5, tl = lane & 31;
-            for (int r = 0; r < row_tiles; ++r) s += sm.red[rb][r * 2 + th][tl];
+            // every row tile's sum read at once (the LDS reads of a loop would each wait on
+            // the previous add); unused tiles add +0, in the same order
+#pragma unroll
+            for (int r = 0; r < (HALVES == 1 ? MAX_RT / 2 : MAX_RT); ++r) {
+                const float x = sm.red[rb][r * 2 + th][tl];
+                s += r < row_tiles ? x : 0.f;
+            }
             bool live = true;
             if (a.pre.mask) live = a.pre.mask[(int64_t)bh * end + j] != 0;
             const float m = live ? s * inv_r2 : 0.f;
@@ -619,7 +632,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         uint16_t *Ks = sm.u.kt[kb].k;
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const int u = tid + j * NT;
+            const int u = item(j);
             if (u < NIK) {
                 if constexpr (SRC == SRC_PACKED) kp_store<D>(Ks, w[j], u);
                 else kd_store<D>(Ks, w[j], u, a.pre.fdtype);
