@@ -313,6 +313,7 @@ struct ScoreSmem {
     int cnt[MAX_R];             // per row r < R: how many selection rows it is
     float rowc[MAX_R];          // per row r < R: M_p*log2e + log2(L_p), +inf when L_p = 0
     int qr[MAX_R2];             // q_rows (T2 <= MAX_R2 entries)
+    uint4 qx[MAX_RT / 2][D / 16][64];   // Q fragments of each row tile (two S units share one)
 };
 
 // Every wave does both jobs, in lock step: S units (a 32-row tile x a 32-token half of a
@@ -432,6 +433,42 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         return min(max(ident ? a.row0 + rr - g * T2 : sm.qr[rr - g * T2], 0), T - 1);
     };
     const int rt_pad = 32 * row_tiles;
+    // Q of the unit's row tile: in-order rows need no table, so their loads are issued
+    // here, before the tables below wait on M_p / L_p (one round trip for all of them)
+    // With two S units per row tile (HALVES == 1: one per 32-token half) each loads half of
+    // the row tile's fragments (k-steps th0 * NKS/2 ..) into qf[0 .. NKS/2) and the halves
+    // are exchanged through LDS before the first tile (share_q).
+    bf16x8_t qf[NKS];
+    constexpr int QH = HALVES == 1 ? NKS / 2 : NKS;   // fragments loaded by this unit
+    auto load_q = [&](int qo) {
+        const int64_t qb = b * a.q.s[0] + (int64_t)h * a.G * a.q.s[1] + (qo < 0 ? 0 : qo);
+        const int ks0 = HALVES == 1 ? th0 * QH : 0;
+#pragma unroll
+        for (int j = 0; j < QH; ++j) qf[j] = ma_load8_as_bf16(a.q.ptr, qb + (ks0 + j) * 16 + hf * 8, a.q.dtype);
+    };
+    if (s_wave && ident) {
+        const int rr = rt * 32 + c32, g = rr / T2;
+        load_q(rr < R2 ? g * (int)a.q.s[1] + sel_pos(rr, g) * (int)a.q.s[2] : -1);
+    }
+    // the value centre's first batch of O_p rows (rows osl, osl + CS, ... of channels
+    // 8 och .. 8 och + 7), also in flight before the tables wait
+    constexpr int CB = 4;
+    constexpr int CS = NT / CH;
+    const int osl = tid / CH, och = tid % CH;
+    uint4 craw[CB], chi[CB];
+    auto load_centre = [&](int r0) {
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+            const int64_t off_o = ((int64_t)bh * R + min(r0 + j * CS, R - 1)) * D + och * 8;
+            if (a.op_dtype == MA_F32) {
+                craw[j] = *(const uint4 *)((const float *)a.op + off_o);
+                chi[j] = *(const uint4 *)((const float *)a.op + off_o + 4);
+            } else {
+                craw[j] = *(const uint4 *)((const uint16_t *)a.op + off_o);
+            }
+        }
+    };
+    if (value && osl < R) load_centre(osl);
     if (ident) {
         for (int rr = tid; rr < rt_pad; rr += NT) {
             float c = __builtin_inff();
@@ -472,54 +509,30 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         }
         __syncthreads();
     }
-    bf16x8_t qf[NKS];
-    if (s_wave) {
-        int qo;
-        if (ident) {
-            const int rr = rt * 32 + c32, g = rr / T2;
-            qo = rr < R2 ? g * (int)a.q.s[1] + sel_pos(rr, g) * (int)a.q.s[2] : -1;
-        } else {
-            qo = sm.qoff[rt * 32 + c32];
-        }
-        const int64_t qb = b * a.q.s[0] + (int64_t)h * a.G * a.q.s[1] + (qo < 0 ? 0 : qo);
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
-    }
+    if (s_wave && !ident) load_q(sm.qoff[rt * 32 + c32]);
 
     // value centre: centre[d] = (1/R2) * sum over rows r of cnt[r] * f32(O_p[r][d]), rows of
     // a slot in ascending order, then slots in groups of 8, then the groups
     if (value) {
-        const int osl = tid / CH, och = tid % CH;
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-        // rows osl, osl + S, ... of channels 8 och .. 8 och + 7, in batches of CB rows whose
-        // loads are in flight together; a row counts as often as it is a selection row (in
-        // order: every row once); rows past R count 0 (their address is clamped)
-        constexpr int CB = 4;
-        constexpr int S = NT / CH;
-        for (int r0 = osl; r0 < R; r0 += CB * S) {
-            uint4 raw[CB];
+        // rows osl, osl + CS, ... of channels 8 och .. 8 och + 7, in batches of CB rows whose
+        // loads are in flight together (the first batch was issued before the tables); a
+        // row counts as often as it is a selection row (in order: every row once); rows past
+        // R count 0 (their address is clamped)
+        for (int r0 = osl; r0 < R; r0 += CB * CS) {
+            if (r0 != osl) load_centre(r0);
+            const uint4 *raw = craw, *hi = chi;
             float wgt[CB];
 #pragma unroll
             for (int j = 0; j < CB; ++j) {
-                const int r = r0 + j * S;
+                const int r = r0 + j * CS;
                 const int tpos = r % T - a.row0;
                 wgt[j] = r >= R ? 0.f : ident ? (tpos >= 0 && tpos < T2 ? 1.f : 0.f) : (float)sm.cnt[r];
-                const int64_t off_o = ((int64_t)bh * R + min(r, R - 1)) * D + och * 8;
-                if (a.op_dtype == MA_F32) {
-                    raw[j] = *(const uint4 *)((const float *)a.op + off_o);
-                } else {
-                    raw[j] = *(const uint4 *)((const uint16_t *)a.op + off_o);
-                }
             }
             if (a.op_dtype == MA_F32) {
-                // f32 rows: the second half of the 8 channels (the first came with raw[j])
-                uint4 hi[CB];
-#pragma unroll
-                for (int j = 0; j < CB; ++j)
-                    hi[j] = *(const uint4 *)((const float *)a.op +
-                                             ((int64_t)bh * R + min(r0 + j * S, R - 1)) * D + och * 8 + 4);
+                // f32 rows: 8 channels in two 16-byte halves
 #pragma unroll
                 for (int j = 0; j < CB; ++j) {
                     const uint32_t wv[8] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
@@ -547,9 +560,29 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         const int rr = rt * 32 + c32;
         if (rr >= R2) {
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = bf16x8_t{};
+            for (int j = 0; j < QH; ++j) qf[j] = bf16x8_t{};
+        }
+        if constexpr (HALVES == 1) {
+#pragma unroll
+            for (int j = 0; j < QH; ++j) sm.qx[rt][th0 * QH + j][lane] = __builtin_bit_cast(uint4, qf[j]);
         }
     }
+    // after a barrier: the other unit's half of the row tile's fragments, in k-step order
+    auto share_q = [&]() {
+        if constexpr (HALVES == 1) {
+            if (s_wave) {
+                if (th0 == 0) {
+#pragma unroll
+                    for (int j = 0; j < QH; ++j) qf[QH + j] = __builtin_bit_cast(bf16x8_t, sm.qx[rt][QH + j][lane]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < QH; ++j) qf[QH + j] = qf[j];
+#pragma unroll
+                    for (int j = 0; j < QH; ++j) qf[j] = __builtin_bit_cast(bf16x8_t, sm.qx[rt][j][lane]);
+                }
+            }
+        }
+    };
 
     // ---- S unit: tile in K buffer kb into the unit's token sums red[rb]
     auto s_tile = [&](int kb, int rb) {
@@ -619,6 +652,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
             }
         }
         __syncthreads();
+        share_q();
         if (s_wave) s_tile(0, 0);
         __syncthreads();
         if (wave == NWV - 1) finish(tile0, 0, 0);
@@ -652,6 +686,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     stage(0, 0);
     if (ntiles > 1) load(1);
     __syncthreads();
+    share_q();
 
     for (int i = 0; i < ntiles; ++i) {
         if (s_wave) s_tile(i & 1, i & 1);
