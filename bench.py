@@ -170,8 +170,8 @@ def main():
         bench_substep(a)
         return
     from maskahead_amd import _native as N
-    from maskahead_amd.kernels import (gather_packed_kv, prefix_scores, quantize_key_groups_into,
-                                       quantize_values_into, splitk_attention, topk_ascending)
+    from maskahead_amd.kernels import (gather_packed_kv, prefix_scores, prefix_scores_topk,
+                                       quantize_key_groups_into, quantize_values_into, splitk_attention)
     from maskahead_amd.kernels.splitk import Prefix
     from maskahead_amd.workloads import CONFIGS, layer_inputs, packed_layout
 
@@ -223,8 +223,8 @@ def main():
 
     def layer_step(L):
         out, stats = splitk_attention(qg, L["prefix"], kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
-        mass, score = prefix_scores(qg, L["prefix"], stats, rows, value=True)
-        idx = topk_ascending(score, sh.read_k)
+        # the score pass also builds the select's first histogram level (one launch less)
+        mass, score, idx = prefix_scores_topk(qg, L["prefix"], stats, rows, sh.read_k, value=True, rank="score")
         gather_packed_kv(L["view"], idx, out_key=L["ck"][:, :, :sh.read_k], out_value=L["cv"][:, :, :sh.read_k])
         result["out"], result["idx"] = out, idx
 
@@ -640,7 +640,7 @@ def extra_c1_block(a):
     top-k of 2 048, gather into the compact buffer) and the block's 3 further denoising
     sub-steps over [2 048 selected | block] (session.py:1403-1454, 1286-1336).  28 layers,
     each with its own cache, in one HIP graph."""
-    from maskahead_amd.kernels import gather_packed_kv, prefix_scores, splitk_attention, topk_ascending
+    from maskahead_amd.kernels import gather_packed_kv, prefix_scores_topk, splitk_attention
     from maskahead_amd.kernels.splitk import Prefix
     from maskahead_amd.workloads import CONFIGS, layer_inputs
 
@@ -674,8 +674,7 @@ def extra_c1_block(a):
     def step():
         for pre, view, ck, cv in layers:
             _, stats = splitk_attention(qg, pre, kcg, vcg, want_prefix=True)
-            _, score = prefix_scores(qg, pre, stats, rows, value=True)
-            idx = topk_ascending(score, sh.read_k)
+            _, score, idx = prefix_scores_topk(qg, pre, stats, rows, sh.read_k, value=True, rank="score")
             gather_packed_kv(view, idx, out_key=ck, out_value=cv)
             sel = Prefix.dense(ck, cv)
             for _ in range(subs):

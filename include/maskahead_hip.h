@@ -79,13 +79,13 @@ typedef struct ma_tensor4 {
 const char *ma_last_error(void);
 int ma_version(void);
 
-/* a3. dequantize_prefix (splitk.py:465-480; codec reference.py:48-55, 168-179, 259-268):
+/* dequantize_prefix (splitk.py:465-480; codec reference.py:48-55, 168-179, 259-268):
  * the whole prefix as [B,H,n,D] K and V in out dtype (bf16 or f32), n = nq + nf.
  * Bit-exact: x = f32(code)*f32(scale) + f32(zero), rounded to nearest even. */
 int ma_dequant_prefix(const ma_prefix *p, int B, int H, int D, ma_tensor4 k_out, ma_tensor4 v_out,
                       void *stream);
 
-/* a4 + a5. splitk_attention (splitk.py:493-579): softmax over [prefix | current] for all
+/* splitk_attention (splitk.py:493-579): softmax over [prefix | current] for all
  * R = (Hq/H)*T rows of every KV head.  Pass 1 writes per-split partials (max, sum and the
  * normalized output on a per-row f16 scale) into `workspace`, pass 2 merges them
  * (log-sum-exp) into `out` [B,Hq,T,D] and, when mp is not NULL, the prefix-only
@@ -126,12 +126,12 @@ int ma_splitk_attention_noalloc(ma_tensor4 q, int B, int Hq, int T, int D, const
                                 int c_pos0, float scale, ma_tensor4 out, float *mp, float *lp, void *op,
                                 int split_tokens, void *stream);
 
-/* a6 (centre). The value centre of prefix_scores (splitk.py:599-601):
+/* The value centre of prefix_scores (splitk.py:599-601):
  * centre[b,h,:] = mean over g < G, t in q_rows of f32(op[b,h,g*T+t,:]); op dtype op_dtype. */
 int ma_value_centre(const void *op, int op_dtype, int B, int H, int G, int T, int D,
                     const int32_t *q_rows, int T2, float *centre, void *stream);
 
-/* a6. prefix_scores (splitk.py:582-614, kernel 321-371): per prefix entry j,
+/* prefix_scores (splitk.py:582-614, kernel 321-371): per prefix entry j,
  * mass[j] = mean over the G*T2 selection rows of exp(s_rj - mp[r]) / lp[r] (0 on dead
  * slots) and, when value != 0, score[j] = mass[j] * ||v_j - centre|| (0 on dead slots),
  * centre as ma_value_centre computes it from op (the prefix-only output of
@@ -148,7 +148,7 @@ int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix 
                      int op_dtype, float scale, int value, int v_round, float *mass, float *score,
                      void *stream);
 
-/* a6v. The score pass of ma_prefix_scores for few selection rows per KV head (the
+/* The score pass of ma_prefix_scores for few selection rows per KV head (the
  * reference serves every row count with BLOCK_M-row tl.dot tiles, splitk.py:321-371): a
  * GQA-reduced VALU pass for at most 16 rows (G*T2 <= 16) -- waves stream 32-token units
  * with no workgroup barrier, q . k by v_dot2c_f32_bf16 for every selection row, the value
@@ -159,7 +159,7 @@ int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix 
  * for a bad mode.  No counterpart in the reference (Triton picks no variant). */
 int ma_prefix_scores_path(int mode);
 
-/* a9. read-set top-k (session.py:1429-1438, reference.py:369-393): for each of `rows`
+/* read-set top-k (session.py:1429-1438, reference.py:369-393): for each of `rows`
  * rows, the k largest of rank[row, 0..n) -- dead slots (mask 0) rank -inf, ties go to
  * the smaller index, -0.0 equals +0.0 and NaN ranks above +inf -- written as ascending
  * int64 indices to idx[row*idx_stride + i]; values (optional, [rows][k] contiguous) gets
@@ -177,7 +177,25 @@ int ma_topk_select(const float *rank, int64_t rank_stride, const uint8_t *mask, 
                    void *state, int64_t state_bytes, void *workspace, int64_t workspace_bytes,
                    void *stream);
 
-/* a10. keep set of an eviction step (EvictionState.survivors, eviction.py:325-409, for the
+/* prefix_scores with the read-set top-k's first level built in.  No counterpart in the
+ * reference (which runs its prefix-score op and then torch.topk, session.py:1418-1438):
+ * ma_prefix_scores, and besides the outputs it builds the read-set top-k's first-level
+ * histogram of rank 1 (the mass) or 2 (the score, value=1)
+ * under the prefix's mask into `topk_state` (zero before, ma_topk_state_bytes(B*H) bytes,
+ * 256-byte aligned).  The caller then runs ma_topk_select_hist_ready on that rank with the
+ * prefix's mask and the same state, which skips the select's histogram launch and leaves
+ * the state zero again: the pair returns what ma_prefix_scores + ma_topk_select return,
+ * with one launch less. */
+int ma_prefix_scores_hist(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
+                          const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
+                          int op_dtype, float scale, int value, int v_round, float *mass, float *score,
+                          int rank, void *topk_state, int64_t state_bytes, void *stream);
+int ma_topk_select_hist_ready(const float *rank, int64_t rank_stride, const uint8_t *mask,
+                              int64_t mask_stride, int rows, int n, int k, int64_t *idx, int64_t idx_stride,
+                              float *values, void *state, int64_t state_bytes, void *workspace,
+                              int64_t workspace_bytes, void *stream);
+
+/* keep set of an eviction step (EvictionState.survivors, eviction.py:325-409, for the
  * score-ranked policies; capacity C = EvictionConfig.capacity, eviction.py:200-202): per
  * row (one (layer, batch, KV head) lane of n live entries), the W = min(window, C) newest
  * entries plus the top (C - W) of score among the others, where positions < sink_tokens
@@ -195,7 +213,7 @@ int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const fl
                    int64_t keep_stride, int32_t *status, void *state, int64_t state_bytes, void *workspace,
                    int64_t workspace_bytes, void *stream);
 
-/* a8. value_score (session.py:27-40): score[row, j] = a[row, j] * ||v_j - c||,
+/* value_score (session.py:27-40): score[row, j] = a[row, j] * ||v_j - c||,
  * c = sum_j w_j v_j / max(sum_j w_j, 1e-12), rows = (b, h) of v [B,H,n,D] (strides b, h, n;
  * bf16, f16 or f32).  fp32_mode 0 (the reference default): w = bf16(a) and every step in
  * bf16 arithmetic as the reference's bf16 tensors compute it; fp32_mode 1: the f32 branch
@@ -205,7 +223,7 @@ int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, int B, int H,
                    float *score, int64_t score_stride, void *workspace, int64_t workspace_bytes,
                    void *stream);
 
-/* a13. compaction of survivors (PackedKVCache.compact, cache.py:342-367; compact_tokens,
+/* compaction of survivors (PackedKVCache.compact, cache.py:342-367; compact_tokens,
  * cache.py:659-678; EvictionState.compact, eviction.py:411-418): for every lane (b, h) and
  * i < capacity, row i of each plane becomes the old row keep[b, h, i] -- in place, for any
  * keep (out-of-range entries give zero rows).  A plane p is a token-major tensor: base
@@ -217,12 +235,12 @@ int ma_compact_tokens(void *const *bases, const int64_t *strides, const int32_t 
                       int H, int n, const int64_t *keep, const int64_t skeep[2], int capacity, void *workspace,
                       int64_t workspace_bytes, void *stream);
 
-/* a14. append of a finalized block into a 16-bit cache (PackedKVCache.stage_layer for
+/* append of a finalized block into a 16-bit cache (PackedKVCache.stage_layer for
  * bf16 layouts, cache.py:423-547): dst[b, h, at + t, :] = src[b, h, t, :] for t < T,
  * converted to dst's dtype (round to nearest even). */
 int ma_append_tokens(ma_tensor4 src, ma_tensor4 dst, int B, int H, int T, int D, int at, void *stream);
 
-/* a11. gather_packed_kv (ops.py:570-662, 835-855; oracle reference.py:396-400): the
+/* gather_packed_kv (ops.py:570-662, 835-855; oracle reference.py:396-400): the
  * entries idx[b,h,0..k) of the prefix, dequantized, into k_out / v_out [B,H,k,D]
  * (bf16 or f32).  idx int64 with strides sidx (b, h; i contiguous). */
 int ma_gather_kv(const ma_prefix *p, int B, int H, int D, const int64_t *idx, const int64_t sidx[2],

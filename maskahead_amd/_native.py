@@ -72,6 +72,8 @@ SIGNATURES = {
     "ma_prefix_scores": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _P, _I, _P, _P, _P, _I, _F, _I, _I, _P,
                               _P, _P]),
     "ma_prefix_scores_path": (_I, [_I]),
+    "ma_prefix_scores_hist": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _P, _I, _P, _P, _P, _I, _F, _I, _I, _P,
+                                   _P, _I, _P, _I64, _P]),
     "ma_keep_select": (_I, [_P, _I, _I64, _P, _I64, _I, _I, _I, _I, _I64, _P, _I64, _I64, _I, _P, _I64, _P,
                             _P, _I64, _P, _I64, _P]),
     "ma_value_score_workspace_bytes": (_I64, [_I, _I, _I]),
@@ -82,6 +84,7 @@ SIGNATURES = {
     "ma_topk_state_bytes": (_I64, [_I]),
     "ma_topk_workspace_bytes": (_I64, [_I, _I]),
     "ma_topk_select": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P]),
+    "ma_topk_select_hist_ready": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _P, _I64, _P, _P, _I64, _P, _I64, _P]),
     "ma_gather_kv": (_I, [_PREF, _I, _I, _I, _P, _I64P, _I, _T4, _T4, _P]),
     "ma_quantize_keys": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),
     "ma_quantize_values": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),

@@ -190,3 +190,9 @@ __device__ __forceinline__ uint32_t ma_order_key(float f) {
 }
 
 #define MA_LOG2E 1.4426950408889634f
+
+// ---- the read-set top-k's first digit (13 bits of the order key): shared by the select
+// kernels and the score pass that can build this level's histogram
+constexpr int MA_TOPK_D0_BITS = 13;
+constexpr int MA_TOPK_H0 = 1 << MA_TOPK_D0_BITS;
+constexpr int MA_TOPK_S0 = 32 - MA_TOPK_D0_BITS;

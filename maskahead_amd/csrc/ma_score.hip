@@ -56,6 +56,11 @@ struct ScoreArgs {
     int per;       // tiles per fast workgroup
     int fast_wgs;  // fast workgroups per lane (blockIdx.x below it); then one tail tile each
     float sl2;
+    // the read-set top-k's level-0 histogram of this pass's ranks (ma_topk_select_hist_ready):
+    // 0 none, 1 the mass, 2 the score of every slot (dead slots -inf), counted into
+    // hist[bh][key >> MA_TOPK_S0]
+    int hist_rank;
+    uint32_t *hist;
 };
 
 // ------------------------------------------------------------------ value centre
@@ -297,6 +302,10 @@ __device__ __forceinline__ float token_sum(float v) {
 }
 
 constexpr int MAX_R = 1024;   // query rows of a KV head (G * T)
+// keys of KEY_TILES tiles are kept in LDS (two blocks, so one is counted into the level-0
+// histogram while the next is written); a workgroup's keys are counted by all of its
+// threads at once, once per block and after the last tile
+constexpr int KEY_TILES = 64;
 
 template <int D, int NT>
 struct ScoreSmem {
@@ -313,7 +322,13 @@ struct ScoreSmem {
     int cnt[MAX_R];             // per row r < R: how many selection rows it is
     float rowc[MAX_R];          // per row r < R: M_p*log2e + log2(L_p), +inf when L_p = 0
     int qr[MAX_R2];             // q_rows (T2 <= MAX_R2 entries)
-    uint4 qx[MAX_RT / 2][D / 16][64];   // Q fragments of each row tile (two S units share one)
+    union {
+        uint4 qx[MAX_RT / 2][D / 16][64];   // (prologue) Q fragments of each row tile
+        struct {
+            uint32_t hist[MA_TOPK_H0];       // (tile loop) the workgroup's level-0 histogram
+            uint32_t keys[2][KEY_TILES * TILE];
+        } hk;
+    } q;
 };
 
 // Every wave does both jobs, in lock step: S units (a 32-row tile x a 32-token half of a
@@ -322,7 +337,7 @@ struct ScoreSmem {
 // workgroup per CU, units of half a tile for up to 16 row tiles) or 512 (two workgroups per
 // CU, so one's memory waits overlap the other's work; up to 8 row tiles, whole-tile units,
 // every thread stages one K item and one V item).
-template <int D, int SRC, int HALVES, int NT>
+template <int D, int SRC, int HALVES, int NT, bool HIST>
 __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     __shared__ ScoreSmem<D, NT> sm;
     constexpr int NWV = NT / 64;                       // waves
@@ -564,7 +579,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         }
         if constexpr (HALVES == 1) {
 #pragma unroll
-            for (int j = 0; j < QH; ++j) sm.qx[rt][th0 * QH + j][lane] = __builtin_bit_cast(uint4, qf[j]);
+            for (int j = 0; j < QH; ++j) sm.q.qx[rt][th0 * QH + j][lane] = __builtin_bit_cast(uint4, qf[j]);
         }
     }
     // after a barrier: the other unit's half of the row tile's fragments, in k-step order
@@ -573,12 +588,12 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
             if (s_wave) {
                 if (th0 == 0) {
 #pragma unroll
-                    for (int j = 0; j < QH; ++j) qf[QH + j] = __builtin_bit_cast(bf16x8_t, sm.qx[rt][QH + j][lane]);
+                    for (int j = 0; j < QH; ++j) qf[QH + j] = __builtin_bit_cast(bf16x8_t, sm.q.qx[rt][QH + j][lane]);
                 } else {
 #pragma unroll
                     for (int j = 0; j < QH; ++j) qf[QH + j] = qf[j];
 #pragma unroll
-                    for (int j = 0; j < QH; ++j) qf[j] = __builtin_bit_cast(bf16x8_t, sm.qx[rt][j][lane]);
+                    for (int j = 0; j < QH; ++j) qf[j] = __builtin_bit_cast(bf16x8_t, sm.q.qx[rt][j][lane]);
                 }
             }
         }
@@ -610,8 +625,10 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     };
 
     const float inv_r2 = 1.0f / (float)a.r2_total;
+    const int hist_rank = HIST ? a.hist_rank : 0;   // HIST: 1 or 2
     auto finish = [&](int tile, int rb, int db) {
         const int j = tile * TILE + lane;
+        uint32_t key = 0u;   // 0: past the end (counted nowhere)
         if (j < end) {
             float s = 0.f;
             const int th = lane >> 5, tl = lane & 31;
@@ -623,11 +640,50 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
                 s += r < row_tiles ? x : 0.f;
             }
             bool live = true;
-            if (a.pre.mask) live = a.pre.mask[(int64_t)bh * end + j] != 0;
+            const int64_t o = (int64_t)bh * end + j;
+            if (a.pre.mask) live = a.pre.mask[o] != 0;
             const float m = live ? s * inv_r2 : 0.f;
-            if (a.accum) a.mass[(int64_t)bh * end + j] += m;
-            else a.mass[(int64_t)bh * end + j] = m;
-            if (value) a.score[(int64_t)bh * end + j] = live ? m * __builtin_sqrtf(sm.dist[db][lane]) : 0.f;
+            const float mf = a.accum ? a.mass[o] + m : m;   // the mass after this pass
+            a.mass[o] = mf;
+            float sc = 0.f;
+            if (value) {
+                sc = live ? m * __builtin_sqrtf(sm.dist[db][lane]) : 0.f;
+                a.score[o] = sc;
+            }
+            // the key ma_topk_select gives this slot under the same mask
+            if constexpr (HIST) key = ma_order_key(live ? (hist_rank == 2 ? sc : mf) : -__builtin_inff());
+        }
+        if constexpr (HIST) {
+            const int r = tile - tile0;   // tile of the run
+            sm.q.hk.keys[(r / KEY_TILES) & 1][(r % KEY_TILES) * TILE + lane] = key;
+        }
+    };
+    // level-0 histogram: cleared (its LDS is the prologue's Q exchange buffer, free after
+    // the first tile's barrier), keys of block kb counted (all threads, LDS atomics), and
+    // the workgroup's nonzero bins added into the row's histogram
+    auto zero_hist = [&]() {
+        for (int i = tid; i < MA_TOPK_H0 / 4; i += NT) ((uint4 *)sm.q.hk.hist)[i] = make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto count_keys = [&](int kb, int tiles) {
+        const uint32_t *ks = sm.q.hk.keys[kb & 1];
+        for (int e = tid; e < tiles * TILE; e += NT) {
+            const uint32_t key = ks[e];
+            if (key) atomicAdd(&sm.q.hk.hist[key >> MA_TOPK_S0], 1u);
+        }
+    };
+    // after the last finish: the blocks not counted in the loop (block kb is counted at
+    // iteration KEY_TILES (kb + 1) + 1 when the run has it), then the flush
+    auto end_hist = [&]() {
+        if (ntiles == 1) zero_hist();   // (no second iteration cleared it)
+        __syncthreads();
+        const int last = (ntiles - 1) / KEY_TILES;
+        for (int kb = ntiles >= KEY_TILES + 2 ? (ntiles - 2) / KEY_TILES : 0; kb <= last; ++kb)
+            count_keys(kb, min(KEY_TILES, ntiles - KEY_TILES * kb));
+        __syncthreads();
+        uint32_t *gh = a.hist + (int64_t)bh * MA_TOPK_H0;
+        for (int i = tid; i < MA_TOPK_H0; i += NT) {
+            const uint32_t x = sm.q.hk.hist[i];
+            if (x) atomicAdd(&gh[i], x);
         }
     };
 
@@ -656,6 +712,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         if (s_wave) s_tile(0, 0);
         __syncthreads();
         if (wave == NWV - 1) finish(tile0, 0, 0);
+        if constexpr (HIST) end_hist();
         return;
     }
 
@@ -689,6 +746,11 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     share_q();
 
     for (int i = 0; i < ntiles; ++i) {
+        if constexpr (HIST) {
+            if (i == 1) zero_hist();
+            // key block kb complete (its last tile finished before the last barrier)
+            if (i >= KEY_TILES + 1 && (i - 1) % KEY_TILES == 0) count_keys((i - 1) / KEY_TILES - 1, KEY_TILES);
+        }
         if (s_wave) s_tile(i & 1, i & 1);
         // staging of tile i + 1, then the loads of tile i + 2
         if (i + 1 < ntiles) {
@@ -700,6 +762,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
         __syncthreads();
     }
     if (wave == NWV - 1) finish(tile0 + ntiles - 1, (ntiles - 1) & 1, (ntiles - 1) % 3);
+    if constexpr (HIST) end_hist();
 }
 
 // ------------------------------------------------------------------ GQA-reduced VALU pass
@@ -1038,11 +1101,13 @@ extern "C" int ma_value_centre(const void *op, int op_dtype, int B, int H, int G
     return ma_check_launch("ma_value_centre");
 }
 
-extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
-                                const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
-                                int op_dtype, float scale, int value, int v_round, float *mass, float *score,
-                                void *stream) {
-    const char *who = "ma_prefix_scores";
+extern "C" int ma_topk_level0_into_state(const float *rank, int64_t rank_stride, const uint8_t *mask,
+                                         int64_t mask_stride, int rows, int n, void *state, void *stream);
+
+static int prefix_scores(const char *who, ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
+                         const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
+                         int op_dtype, float scale, int value, int v_round, float *mass, float *score,
+                         int hist_rank, void *topk_state, int64_t state_bytes, void *stream) {
     int rc = ma_validate_prefix(p, D, who);
     if (rc) return rc;
     if (B <= 0 || H <= 0 || Hq <= 0 || Hq % H || T <= 0 || T2 <= 0 || !q.ptr || (!q_rows && T2 > T) || !mp || !lp ||
@@ -1120,6 +1185,16 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
     }
     sa.vround = v_round;
     sa.sl2 = scale * MA_LOG2E;
+    if (hist_rank) {
+        if ((hist_rank != 1 && hist_rank != 2) || (hist_rank == 2 && !value) || !topk_state ||
+            ((uintptr_t)topk_state & 255) || state_bytes < ma_topk_state_bytes(B * H)) {
+            ma_set_error("%s: rank must be 1 (mass) or 2 (score, value-aware), and the top-k state %lld bytes "
+                         "(256-byte aligned) for %d rows; got rank %d and %lld bytes", who,
+                         (long long)ma_topk_state_bytes(B * H), B * H, hist_rank, (long long)state_bytes);
+            return MA_EINVAL;
+        }
+    }
+    sa.hist = (uint32_t *)topk_state;
     hipStream_t st = (hipStream_t)stream;
     // at most SMALL_ROWS selection rows: the GQA-reduced VALU pass, one pass over the rows
     const int path = g_score_path.load(std::memory_order_relaxed);
@@ -1156,13 +1231,20 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
             else MA_SMALL(64, 16);
         }
 #undef MA_SMALL
-        return ma_check_launch(who);
+        rc = ma_check_launch(who);
+        if (rc || !hist_rank) return rc;
+        // this pass does not build the histogram in-kernel: the select's own level-0 launch
+        return ma_topk_level0_into_state(hist_rank == 2 ? score : mass, n, p->mask, n, B * H, n, topk_state, stream);
     }
     sa.nfast = nfast;
     sa.per = per;
     sa.fast_wgs = fast_wgs;
     dim3 grid(fast_wgs + (tiles - nfast), B * H);
-#define MA_SCORE(D_, S_, H_) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT>), grid, dim3(SNT), 0, st, sa)
+#define MA_SCORE(D_, S_, H_)                                                                     \
+    do {                                                                                         \
+        if (sa.hist_rank) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, true>), grid, dim3(SNT), 0, st, sa); \
+        else hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, false>), grid, dim3(SNT), 0, st, sa);            \
+    } while (0)
 #define MA_SCORE_I(D_, S_)                        \
     do {                                          \
         if (halves == 1) MA_SCORE(D_, S_, 1);     \
@@ -1176,6 +1258,7 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
         sa.R2 = G * t2;
         sa.row_tiles = (G * t2 + 31) / 32;
         sa.accum = t0 > 0;
+        sa.hist_rank = t0 + t2 >= T2 ? hist_rank : 0;   // the last pass sees the final mass
         if (D == 128) {
             if (packed) MA_SCORE_I(128, SRC_PACKED);
             else MA_SCORE_I(128, SRC_DENSE);
@@ -1189,4 +1272,24 @@ extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const
 #undef MA_SCORE_I
 #undef MA_SCORE
     return MA_OK;
+}
+
+extern "C" int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
+                                const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
+                                int op_dtype, float scale, int value, int v_round, float *mass, float *score,
+                                void *stream) {
+    return prefix_scores("ma_prefix_scores", q, B, Hq, T, D, p, H, q_rows, T2, mp, lp, op, op_dtype, scale, value,
+                         v_round, mass, score, 0, nullptr, 0, stream);
+}
+
+extern "C" int ma_prefix_scores_hist(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H,
+                                     const int32_t *q_rows, int T2, const float *mp, const float *lp, const void *op,
+                                     int op_dtype, float scale, int value, int v_round, float *mass, float *score,
+                                     int rank, void *topk_state, int64_t state_bytes, void *stream) {
+    if (rank != 1 && rank != 2) {
+        ma_set_error("ma_prefix_scores_hist: rank must be 1 (mass) or 2 (score), got %d", rank);
+        return MA_EINVAL;
+    }
+    return prefix_scores("ma_prefix_scores_hist", q, B, Hq, T, D, p, H, q_rows, T2, mp, lp, op, op_dtype, scale,
+                         value, v_round, mass, score, rank, topk_state, state_bytes, stream);
 }

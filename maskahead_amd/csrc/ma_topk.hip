@@ -50,6 +50,8 @@ constexpr int NCL = 8192;               // candidates per row kept in LDS beyond
                                         // of a value-aware keep contest at 64k entries holds a few
                                         // thousand); more are re-read from the workspace
 static_assert(D0_BITS + D1_BITS + D2_BITS == 32, "digits cover the key");
+static_assert(D0_BITS == MA_TOPK_D0_BITS && H0 == MA_TOPK_H0 && S0 == MA_TOPK_S0,
+              "the score pass builds level 0 with these digits");
 
 // one row's block of the state buffer
 struct alignas(256) RowState {
@@ -611,19 +613,41 @@ int topk_prepare(TopkArgs &a, int &vpt, const char *who, const float *rank, int6
     return MA_OK;
 }
 
+// hist_ready: the rows' level-0 histograms are already in the state (built by the score
+// pass), so the histogram launch is skipped
 template <bool KEEP>
-int topk_launch(const TopkArgs &a, int rows, int vpt, hipStream_t st, const char *who) {
+int topk_launch(const TopkArgs &a, int rows, int vpt, hipStream_t st, const char *who, bool hist_ready = false) {
     const dim3 grid(a.C, rows);
     if (vpt == 4) {
-        hipLaunchKernelGGL((topk_hist_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
+        if (!hist_ready) hipLaunchKernelGGL((topk_hist_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
         hipLaunchKernelGGL((topk_boundary_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
         hipLaunchKernelGGL((topk_emit_kernel<4, KEEP>), grid, dim3(TB), 0, st, a);
     } else {
-        hipLaunchKernelGGL((topk_hist_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
+        if (!hist_ready) hipLaunchKernelGGL((topk_hist_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
         hipLaunchKernelGGL((topk_boundary_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
         hipLaunchKernelGGL((topk_emit_kernel<16, KEEP>), grid, dim3(TB), 0, st, a);
     }
     return ma_check_launch(who);
+}
+
+int topk_select(const char *who, bool hist_ready, const float *rank, int64_t rank_stride, const uint8_t *mask,
+                int64_t mask_stride, int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values,
+                void *state, int64_t state_bytes, void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!rank || !idx || rows < 0 || n < 0 || k < 0 || k > n || idx_stride < k || rank_stride < n ||
+        (mask && mask_stride < n) || rows > 65535) {
+        ma_set_error("%s: bad arguments (rows=%d n=%d k=%d)", who, rows, n, k);
+        return MA_EINVAL;
+    }
+    if (rows == 0 || k == 0) return MA_OK;
+    TopkArgs a;
+    int vpt = 0;
+    const int rc = topk_prepare(a, vpt, who, rank, rank_stride, rows, n, k, idx, idx_stride, state, state_bytes,
+                                workspace, workspace_bytes);
+    if (rc) return rc;
+    a.mask = mask;
+    a.mask_stride = mask_stride;
+    a.values = values;
+    return topk_launch<false>(a, rows, vpt, (hipStream_t)stream, who, hist_ready);
 }
 
 }  // namespace
@@ -632,21 +656,37 @@ extern "C" int ma_topk_select(const float *rank, int64_t rank_stride, const uint
                               int rows, int n, int k, int64_t *idx, int64_t idx_stride, float *values,
                               void *state, int64_t state_bytes, void *workspace, int64_t workspace_bytes,
                               void *stream) {
-    if (!rank || !idx || rows < 0 || n < 0 || k < 0 || k > n || idx_stride < k || rank_stride < n ||
-        (mask && mask_stride < n) || rows > 65535) {
-        ma_set_error("ma_topk_select: bad arguments (rows=%d n=%d k=%d)", rows, n, k);
-        return MA_EINVAL;
-    }
-    if (rows == 0 || k == 0) return MA_OK;
-    TopkArgs a;
-    int vpt = 0;
-    const int rc = topk_prepare(a, vpt, "ma_topk_select", rank, rank_stride, rows, n, k, idx, idx_stride, state,
-                                state_bytes, workspace, workspace_bytes);
-    if (rc) return rc;
+    return topk_select("ma_topk_select", false, rank, rank_stride, mask, mask_stride, rows, n, k, idx, idx_stride,
+                       values, state, state_bytes, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ma_topk_select_hist_ready(const float *rank, int64_t rank_stride, const uint8_t *mask,
+                                         int64_t mask_stride, int rows, int n, int k, int64_t *idx,
+                                         int64_t idx_stride, float *values, void *state, int64_t state_bytes,
+                                         void *workspace, int64_t workspace_bytes, void *stream) {
+    return topk_select("ma_topk_select_hist_ready", true, rank, rank_stride, mask, mask_stride, rows, n, k, idx,
+                       idx_stride, values, state, state_bytes, workspace, workspace_bytes, stream);
+}
+
+// The level-0 histograms alone, into a state (for the score passes that do not build them
+// in-kernel); part of the library's internals, not of the C ABI header.
+extern "C" int ma_topk_level0_into_state(const float *rank, int64_t rank_stride, const uint8_t *mask,
+                                         int64_t mask_stride, int rows, int n, void *state, void *stream) {
+    const int vpt = topk_vpt(n);
+    if (!vpt || rows <= 0 || !state) return MA_EINVAL;
+    TopkArgs a = TopkArgs{};
+    a.rank = rank;
+    a.rank_stride = rank_stride;
     a.mask = mask;
     a.mask_stride = mask_stride;
-    a.values = values;
-    return topk_launch<false>(a, rows, vpt, (hipStream_t)stream, "ma_topk_select");
+    a.n = n;
+    a.C = (n + TB * vpt - 1) / (TB * vpt);
+    a.vec = ((uintptr_t)rank & 15) == 0 && rank_stride % 4 == 0;
+    a.state = (RowState *)state;
+    const dim3 grid(a.C, rows);
+    if (vpt == 4) hipLaunchKernelGGL((topk_hist_kernel<4, false>), grid, dim3(TB), 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL((topk_hist_kernel<16, false>), grid, dim3(TB), 0, (hipStream_t)stream, a);
+    return ma_check_launch("ma_topk_level0_into_state");
 }
 
 extern "C" int ma_keep_select(const void *pos, int pos_is_i64, int64_t pos_stride, const float *score,

@@ -9,7 +9,7 @@ from .ops import (
     quantize_values_into,
     selector_topk,
 )
-from .select import topk_ascending
+from .select import prefix_scores_topk, topk_ascending
 from .splitk import Prefix, dequantize_prefix, prefix_scores, splitk_attention
 
 __all__ = [
@@ -20,6 +20,7 @@ __all__ = [
     "gather_packed_kv",
     "hip_available",
     "prefix_scores",
+    "prefix_scores_topk",
     "quantize_key_groups_into",
     "quantize_values_into",
     "selector_topk",

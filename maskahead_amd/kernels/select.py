@@ -17,6 +17,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native as N
+from .splitk import prefix_scores   # (splitk does not import this module)
 
 _STATES: dict = {}
 
@@ -82,3 +83,43 @@ def topk_ascending(rank: torch.Tensor, k: int, mask: torch.Tensor | None = None,
                             st.numel(), ws.data_ptr(), ws.numel(), stream)
     N.check(rc, "ma_topk_select")
     return out
+
+
+def prefix_scores_topk(query, prefix, stats, q_rows, k: int, *, value: bool, rank: str = "score",
+                       scaling=None, values: torch.Tensor | None = None):
+    """prefix_scores followed by the read-set top-k over its mass (rank="mass") or score
+    (rank="score", value-aware), masked by the prefix's mask, as session.py:1418-1438 runs
+    them; the score pass builds the top-k's first-level histogram, so the pair costs one
+    launch less than prefix_scores + topk_ascending and returns the same mass, score and
+    indices.  Returns (mass, score, idx); idx int64 [B, Hkv, k] ascending."""
+    if rank not in ("mass", "score") or (rank == "score" and not value):
+        raise ValueError("rank must be 'mass', or 'score' with value=True")
+    used = stats[3] if stats[3] is not None else prefix
+    mp = stats[0]
+    b, hkv, n = mp.shape[0], mp.shape[1], used.n
+    k = int(k)
+    if not 0 <= k <= n:
+        raise ValueError(f"k={k} outside [0, {n}]")
+    idx = torch.empty((b, hkv, k), device=query.device, dtype=torch.int64)
+    if k == 0 or n == 0 or b * hkv == 0:
+        mass, score = prefix_scores(query, prefix, stats, q_rows, value=value, scaling=scaling)
+        return mass, score, idx
+    rows = b * hkv
+    if values is not None and (not values.is_contiguous() or values.numel() != rows * k):
+        raise ValueError("values must be a contiguous f32 [B, Hkv, k] tensor")
+    ws_bytes = N.size_query("ma_topk_workspace_bytes", rows, n)
+    if ws_bytes <= 0:
+        raise N.KernelUnavailableError(f"ma_topk_select: n={n} exceeds the built maximum")
+    stream = N.stream_of(query)
+    st = _state(query.device, N.size_query("ma_topk_state_bytes", rows), stream)
+    code = 2 if rank == "score" else 1
+    mass, score = prefix_scores(query, prefix, stats, q_rows, value=value, scaling=scaling, _topk_hist=(code, st))
+    # mass / score are fresh contiguous [B, Hkv, n] f32; prefix_scores has checked the mask
+    # (contiguous uint8 [B, Hkv, n])
+    r = score if rank == "score" else mass
+    ws = torch.empty((ws_bytes,), device=query.device, dtype=torch.uint8)
+    rc = N.load().ma_topk_select_hist_ready(r.data_ptr(), n, N.ptr(used.mask), n if used.mask is not None else 0,
+                                            rows, n, k, idx.data_ptr(), k, N.ptr(values), st.data_ptr(),
+                                            st.numel(), ws.data_ptr(), ws.numel(), stream)
+    N.check(rc, "ma_topk_select_hist_ready")
+    return mass, score, idx

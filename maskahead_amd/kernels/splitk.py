@@ -222,13 +222,16 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
 
 
 def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: bool, scaling=None,
-                  block_m: int = 64, block_n: int = 64):
+                  block_m: int = 64, block_n: int = 64, _topk_hist=None):
     """Per prefix entry: mass a_j (mean prefix-softmax over the selection rows) and, with
     value=True, a_j * ||v_j - c|| with c the mean of O_p over those rows
     (splitk.py:582-614).  q_rows: block positions of the selection queries -- an int
     tensor (on the GPU: used as given) or a host sequence / CPU tensor (checked; the whole
     block in order takes the kernels' row-table-free path).
-    Returns (mass, score) as [B, Hkv, n] f32 (score None when value=False); dead slots 0."""
+    Returns (mass, score) as [B, Hkv, n] f32 (score None when value=False); dead slots 0.
+    _topk_hist = (rank, state): also build the read-set top-k's first-level histogram of the
+    mass (rank 1) or score (rank 2) into that select state (select.prefix_scores_topk pairs
+    this with the select that empties it again)."""
     b, hq, t, d = query.shape
     mp, lp, op, used = stats
     prefix = used if used is not None else prefix
@@ -260,9 +263,13 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
         raise ValueError("stats O_p must be a contiguous [B, Hkv, R, D] tensor")
     scale = float(scaling) if scaling is not None else d ** -0.5
     vround = int(prefix.vround) if prefix.nq else 0
-    rc = lib.ma_prefix_scores(N.t4(query), b, hq, t, d, prefix.native(), hkv, N.ptr(q_rows), t2,
-                              mp.data_ptr(), lp.data_ptr(), op.data_ptr() if value else None,
-                              N.dtype_code(op.dtype) if value else 0, scale, 1 if value else 0, vround,
-                              mass.data_ptr(), N.ptr(score), st)
-    N.check(rc, "ma_prefix_scores")
+    args = (N.t4(query), b, hq, t, d, prefix.native(), hkv, N.ptr(q_rows), t2, mp.data_ptr(), lp.data_ptr(),
+            op.data_ptr() if value else None, N.dtype_code(op.dtype) if value else 0, scale, 1 if value else 0,
+            vround, mass.data_ptr(), N.ptr(score))
+    if _topk_hist is None:
+        N.check(lib.ma_prefix_scores(*args, st), "ma_prefix_scores")
+    else:
+        rank, state = _topk_hist
+        N.check(lib.ma_prefix_scores_hist(*args, int(rank), state.data_ptr(), state.numel(), st),
+                "ma_prefix_scores_hist")
     return mass, score

@@ -26,7 +26,7 @@ import torch
 
 from .._native import KernelUnavailableError
 from ..kernels.ops import gather_packed_kv
-from ..kernels.select import topk_ascending
+from ..kernels.select import prefix_scores_topk
 from ..kernels.splitk import Prefix, prefix_scores, splitk_attention
 
 
@@ -224,19 +224,22 @@ class FastLayerPath:
             return out
         rows = self.rows(self.query_indices)
         value = need_sel and self.value_aware
-        mass, score = prefix_scores(query, prefix, stats, rows, value=value, scaling=scale)
-        if need_mass:
-            self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
         if need_sel:
             k = min(int(topk), prefix.n)
             if k <= 0:
                 raise ValueError("the read budget must be positive")
-            state = self.ensure_state(layer_idx, k)
-            rank = score if value else mass
             if not self.sort_indices:
                 raise KernelUnavailableError("the HIP read-set select returns ascending indices only "
                                              "(selector.sort_indices = False is not built)")
-            idx = topk_ascending(rank, k, prefix.mask)
+            # the score pass builds the select's first histogram level (one launch less)
+            mass, score, idx = prefix_scores_topk(query, prefix, stats, rows, k, value=value,
+                                                  rank="score" if value else "mass", scaling=scale)
+        else:
+            mass, score = prefix_scores(query, prefix, stats, rows, value=value, scaling=scale)
+        if need_mass:
+            self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
+        if need_sel:
+            state = self.ensure_state(layer_idx, k)
             gather_packed_kv(self.cache.layer_view(layer_idx), idx, dtype=self.compute_dtype,
                              out_key=state.key[:, :, :k, :], out_value=state.value[:, :, :k, :])
             state.indices = idx
