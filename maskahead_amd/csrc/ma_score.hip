@@ -349,7 +349,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     constexpr int NW = SRC == SRC_PACKED ? 4 : 8;      // staging words per item
     constexpr int CH = D / 8;                          // 8-channel chunks of a row
 
-    const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    const int h = blockIdx.y, b = blockIdx.z, bh = b * a.H + h;   // (no scalar division)
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
     const bool value = a.value;
@@ -1165,7 +1165,7 @@ static int prefix_scores(const char *who, ma_tensor4 q, int B, int Hq, int T, in
     const int fast_wgs = nfast > 0 ? (nfast + per - 1) / per : 0;
     ScoreArgs sa{};
     sa.q = q;
-    sa.pre = prefix_dev(p);
+    sa.pre = prefix_dev(p, B, H);
     sa.q_rows = q_rows;
     sa.mp = mp;
     sa.lp = lp;
@@ -1239,7 +1239,7 @@ static int prefix_scores(const char *who, ma_tensor4 q, int B, int Hq, int T, in
     sa.nfast = nfast;
     sa.per = per;
     sa.fast_wgs = fast_wgs;
-    dim3 grid(fast_wgs + (tiles - nfast), B * H);
+    dim3 grid(fast_wgs + (tiles - nfast), H, B);
 #define MA_SCORE(D_, S_, H_)                                                                     \
     do {                                                                                         \
         if (sa.hist_rank) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, true>), grid, dim3(SNT), 0, st, sa); \

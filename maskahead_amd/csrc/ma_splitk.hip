@@ -874,7 +874,7 @@ int make_plan(Plan &pl, const char *who, ma_tensor4 q, int B, int Hq, int T, int
     _Float16 *wo = (_Float16 *)(((uintptr_t)(wsc + rows) + 15) & ~(uintptr_t)15);
     FwdArgs &fa = pl.fa;
     fa.q = q;
-    fa.pre = prefix_dev(p);
+    fa.pre = prefix_dev(p, B, H);
     fa.kc = kc;
     fa.vc = vc;
     fa.H = H;

@@ -54,10 +54,14 @@ struct PrefixDev {
     const void *kf, *vf;
     const uint8_t *mask;
     int64_t skq[4], sks[3], svq[4], svs[3], skf[3], svf[3];
-    int nq, nf, fdtype;
+    // the (b, h) strides of kq, ks (and kz), vq, vs (and vz), kf, vf as 32-bit values, set
+    // when every lane's offset b * s[0] + h * s[1] fits in 31 bits (off32): the lane bases
+    // then take 32-bit scalar multiplies instead of 64-bit ones in every wave
+    int32_t lo32[6][2];
+    int nq, nf, fdtype, off32;
 };
 
-inline PrefixDev prefix_dev(const ma_prefix *p) {
+inline PrefixDev prefix_dev(const ma_prefix *p, int B, int H) {
     PrefixDev a;
     a.kq = (const uint8_t *)p->kq;
     a.ks = (const uint16_t *)p->ks;
@@ -81,6 +85,16 @@ inline PrefixDev prefix_dev(const ma_prefix *p) {
     a.nq = p->nq;
     a.nf = p->nf;
     a.fdtype = p->fdtype;
+    const int64_t *ls[6] = {p->skq, p->sks, p->svq, p->svs, p->skf, p->svf};
+    a.off32 = 1;
+    for (int i = 0; i < 6; ++i) {
+        const int64_t s0 = ls[i][0], s1 = ls[i][1];
+        const bool fits = s0 >= 0 && s1 >= 0 && s0 <= INT32_MAX && s1 <= INT32_MAX &&
+                          (int64_t)(B - 1) * s0 + (int64_t)(H - 1) * s1 <= INT32_MAX;
+        a.off32 &= fits ? 1 : 0;
+        a.lo32[i][0] = fits ? (int32_t)s0 : 0;
+        a.lo32[i][1] = fits ? (int32_t)s1 : 0;
+    }
     return a;
 }
 
@@ -102,14 +116,31 @@ __device__ __forceinline__ Lane make_lane(const PrefixDev &a, int b, int h, int 
     L.ntot = a.nq + a.nf;
     L.fdtype = a.fdtype;
     L.esz = a.fdtype == MA_F32 ? 4 : 2;
-    L.kq = a.kq + b * a.skq[0] + h * a.skq[1];
-    L.ks = a.ks + b * a.sks[0] + h * a.sks[1];
-    L.kz = a.kz + b * a.sks[0] + h * a.sks[1];
-    L.vq = a.vq + b * a.svq[0] + h * a.svq[1];
-    L.vs = a.vs + b * a.svs[0] + h * a.svs[1];
-    L.vz = a.vz + b * a.svs[0] + h * a.svs[1];
-    L.kf = (const char *)a.kf + (b * a.skf[0] + h * a.skf[1]) * L.esz;
-    L.vf = (const char *)a.vf + (b * a.svf[0] + h * a.svf[1]) * L.esz;
+    if (a.off32) {
+        const uint32_t okq = (uint32_t)(b * a.lo32[0][0] + h * a.lo32[0][1]);
+        const uint32_t oks = (uint32_t)(b * a.lo32[1][0] + h * a.lo32[1][1]);
+        const uint32_t ovq = (uint32_t)(b * a.lo32[2][0] + h * a.lo32[2][1]);
+        const uint32_t ovs = (uint32_t)(b * a.lo32[3][0] + h * a.lo32[3][1]);
+        const uint32_t okf = (uint32_t)(b * a.lo32[4][0] + h * a.lo32[4][1]);
+        const uint32_t ovf = (uint32_t)(b * a.lo32[5][0] + h * a.lo32[5][1]);
+        L.kq = a.kq + okq;
+        L.ks = a.ks + oks;
+        L.kz = a.kz + oks;
+        L.vq = a.vq + ovq;
+        L.vs = a.vs + ovs;
+        L.vz = a.vz + ovs;
+        L.kf = (const char *)a.kf + (uint64_t)okf * L.esz;
+        L.vf = (const char *)a.vf + (uint64_t)ovf * L.esz;
+    } else {
+        L.kq = a.kq + b * a.skq[0] + h * a.skq[1];
+        L.ks = a.ks + b * a.sks[0] + h * a.sks[1];
+        L.kz = a.kz + b * a.sks[0] + h * a.sks[1];
+        L.vq = a.vq + b * a.svq[0] + h * a.svq[1];
+        L.vs = a.vs + b * a.svs[0] + h * a.svs[1];
+        L.vz = a.vz + b * a.svs[0] + h * a.svs[1];
+        L.kf = (const char *)a.kf + (b * a.skf[0] + h * a.skf[1]) * L.esz;
+        L.vf = (const char *)a.vf + (b * a.svf[0] + h * a.svf[1]) * L.esz;
+    }
     L.mask = a.mask ? a.mask + (int64_t)bh * L.ntot : nullptr;
     L.kq_g = (int)a.skq[2];
     L.kq_d = (int)a.skq[3];
