@@ -337,7 +337,7 @@ struct ScoreSmem {
 // workgroup per CU, units of half a tile for up to 16 row tiles) or 512 (two workgroups per
 // CU, so one's memory waits overlap the other's work; up to 8 row tiles, whole-tile units,
 // every thread stages one K item and one V item).
-template <int D, int SRC, int HALVES, int NT, bool HIST>
+template <int D, int SRC, int HALVES, int NT, bool HIST, bool LANE32>
 __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     __shared__ ScoreSmem<D, NT> sm;
     constexpr int NWV = NT / 64;                       // waves
@@ -385,7 +385,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
     int64_t kq_tile = 0, ks_tile = 0, vq_tile = 0, vs_tile = 0, kf_tile = 0, vf_tile = 0;
     int kq_d = 0;
     if (fast) {
-        const Lane L = make_lane(a.pre, b, h, bh);
+        const Lane L = make_lane<LANE32 ? 1 : 0>(a.pre, b, h, bh);
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const int u = item(j);
@@ -689,7 +689,7 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
 
     if (!fast) {
         // ---- tail workgroup: one tile, staged element-wise by every thread
-        const Lane L = make_lane(a.pre, b, h, bh);
+        const Lane L = make_lane<LANE32 ? 1 : 0>(a.pre, b, h, bh);
         const int n0 = tile0 * TILE;
         uint16_t *Ks = sm.u.kt[0].k;
 #pragma unroll 1
@@ -1240,10 +1240,11 @@ static int prefix_scores(const char *who, ma_tensor4 q, int B, int Hq, int T, in
     sa.per = per;
     sa.fast_wgs = fast_wgs;
     dim3 grid(fast_wgs + (tiles - nfast), H, B);
-#define MA_SCORE(D_, S_, H_)                                                                     \
-    do {                                                                                         \
-        if (sa.hist_rank) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, true>), grid, dim3(SNT), 0, st, sa); \
-        else hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, false>), grid, dim3(SNT), 0, st, sa);            \
+#define MA_SCORE(D_, S_, H_)                                                                          \
+    do {                                                                                              \
+        if (!sa.pre.off32) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, false, false>), grid, dim3(SNT), 0, st, sa); \
+        else if (sa.hist_rank) hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, true, true>), grid, dim3(SNT), 0, st, sa); \
+        else hipLaunchKernelGGL((score_kernel<D_, S_, H_, SNT, false, true>), grid, dim3(SNT), 0, st, sa);                  \
     } while (0)
 #define MA_SCORE_I(D_, S_)                        \
     do {                                          \
@@ -1271,6 +1272,9 @@ static int prefix_scores(const char *who, ma_tensor4 q, int B, int Hq, int T, in
     }
 #undef MA_SCORE_I
 #undef MA_SCORE
+    // lanes beyond 31-bit offsets run the kernel without the in-kernel histogram
+    if (hist_rank && !sa.pre.off32)
+        return ma_topk_level0_into_state(hist_rank == 2 ? score : mass, n, p->mask, n, B * H, n, topk_state, stream);
     return MA_OK;
 }
 

@@ -110,13 +110,17 @@ struct Lane {
     int nq, ntot, fdtype, esz;  // esz: bytes per element of the 16/32-bit part
 };
 
+// LANE32: 1 -- the 32-bit lane offsets only (the caller has checked a.off32), 0 -- the
+// 64-bit ones only, -1 -- chosen by a.off32 at run time.  A kernel compiled for one kind
+// alone carries fewer scalar registers than one with both.
+template <int LANE32 = -1>
 __device__ __forceinline__ Lane make_lane(const PrefixDev &a, int b, int h, int bh) {
     Lane L;
     L.nq = a.nq;
     L.ntot = a.nq + a.nf;
     L.fdtype = a.fdtype;
     L.esz = a.fdtype == MA_F32 ? 4 : 2;
-    if (a.off32) {
+    if (LANE32 == 1 || (LANE32 < 0 && a.off32)) {
         const uint32_t okq = (uint32_t)(b * a.lo32[0][0] + h * a.lo32[0][1]);
         const uint32_t oks = (uint32_t)(b * a.lo32[1][0] + h * a.lo32[1][1]);
         const uint32_t ovq = (uint32_t)(b * a.lo32[2][0] + h * a.lo32[2][1]);

@@ -2,12 +2,14 @@
 head) lane's base pointers with 32-bit products when every lane offset of the prefix fits
 in 31 bits and with 64-bit ones otherwise.  Here batch 1 of the packed keys lies 2 GiB past
 batch 0 (its lane offsets exceed 2^31 bytes, so the 64-bit path runs); the attention
-output, the prefix statistics and the scores must be bit-identical to those of the same
-prefix stored compactly (the 32-bit path)."""
+output, the prefix statistics, the scores and the read set of the fused score + select
+(whose first histogram level the 64-bit score kernel leaves to the select's own launch)
+must be bit-identical to those of the same prefix stored compactly (the 32-bit path)."""
 
 import pytest
 import torch
 
+from maskahead_amd.kernels import prefix_scores_topk
 from maskahead_amd.kernels.splitk import Prefix, prefix_scores, splitk_attention
 
 from _util import gpu_prefix, layer_inputs, packed_cpu
@@ -42,4 +44,9 @@ def test_lane_offsets_beyond_31_bits(gpu):
     m_w, s_w = prefix_scores(qg, wide, st_w, rows, value=True)
     assert torch.equal(m_c, m_w)
     assert torch.equal(s_c, s_w)
+    fm_c, fs_c, idx_c = prefix_scores_topk(qg, compact, st_c, rows, 300, value=True)
+    fm_w, fs_w, idx_w = prefix_scores_topk(qg, wide, st_w, rows, 300, value=True)
+    assert torch.equal(fs_c, s_c) and torch.equal(fs_w, s_w)
+    assert torch.equal(idx_c, idx_w)
+    assert torch.equal(idx_c, torch.topk(s_c, 300).indices.sort(-1).values)
     del big, far
