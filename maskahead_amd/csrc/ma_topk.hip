@@ -46,6 +46,8 @@ constexpr int H1 = 1 << D1_BITS;        // 2048 level-1 bins
 constexpr int H2 = 1 << D2_BITS;        // 256 level-2 bins
 constexpr int MAX_CHUNKS = 1024;        // per row (4 chunks per thread in the chunk scans)
 constexpr int NCR = 8;                  // candidates per thread kept in registers by the emit kernel
+constexpr int SPEC_C = 64;              // read-set rows of up to this many chunks read their candidate
+constexpr int SPEC_N = 8 * TB;          // slots speculatively (SPEC_N / C per chunk, see the emit kernel)
 constexpr int NCL = 8192;               // candidates per row kept in LDS beyond that (a boundary bin
                                         // of a value-aware keep contest at 64k entries holds a few
                                         // thousand); more are re-read from the workspace
@@ -75,7 +77,7 @@ struct TopkArgs {
     float *values;
     RowState *state;     // [rows]
     ChunkInfo *chunk;    // [rows][C]
-    uint2 *cand;         // [rows][C][CS]: (key, index) per chunk
+    uint32_t *cand;      // [rows][C][CS]: the candidates' keys per chunk (in index order)
     // keep set: positions (int32 or int64) and the sink / pin rules; keys of entries j >= m
     // (the W newest) are 0, so they never contest and are appended after the selection
     const void *pos;
@@ -272,12 +274,12 @@ __global__ void __launch_bounds__(TB) topk_boundary_kernel(TopkArgs a) {
         packed[0] += key[e] && d == d0 ? 0x10000u : 0u;
     }
     const uint32_t total = block_prefix_runs<1>(packed, wsum);
-    uint2 *L = a.cand + ((int64_t)row * a.C + c) * CS;
+    uint32_t *L = a.cand + ((int64_t)row * a.C + c) * CS;
     uint32_t pos = packed[0] >> 16;
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
         if (key[e] && (key[e] >> S0) == d0) {
-            L[pos] = make_uint2(key[e], (uint32_t)chunk_index<VPT>(c, e));
+            L[pos] = key[e];
             ++pos;
         }
     }
@@ -292,14 +294,49 @@ __global__ void __launch_bounds__(TB) topk_boundary_kernel(TopkArgs a) {
     }
 }
 
+// One wave: the bin d of the LDS histogram h[0, 64 PB) with count(bins above d) < kk <=
+// count(bins >= d), and that count of bins above d (d = above = 0 should kk exceed the
+// total).  Lane l sums bins [l PB, (l + 1) PB); a lane scan finds the lane holding d, and a
+// second one over that lane's PB bins, one per lane, the bin.  All 64 lanes must be active.
+template <int PB>
+__device__ __forceinline__ void wave_find_digit(const uint32_t *h, uint32_t kk, uint32_t &d, uint32_t &above) {
+    static_assert(PB % 4 == 0 && PB <= 64, "bins per lane");
+    const int ln = lane_id();
+    uint32_t s = 0u;
+#pragma unroll
+    for (int q = 0; q < PB / 4; ++q) {
+        const uint4 x = ((const uint4 *)h)[ln * (PB / 4) + q];
+        s += (x.x + x.y) + (x.z + x.w);
+    }
+    uint32_t incl = ma_wave_prefix_u32(s);
+    const uint32_t ab = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) - incl;   // bins of later lanes
+    d = 0u;
+    above = 0u;
+    const uint64_t m = __ballot(ab < kk && ab + s >= kk);
+    if (!m) return;
+    const int L = __builtin_ctzll(m);
+    const uint32_t abl = (uint32_t)__builtin_amdgcn_readlane((int)ab, L);
+    const uint32_t x = ln < PB ? h[L * PB + ln] : 0u;
+    incl = ma_wave_prefix_u32(x);
+    const uint32_t ab2 = abl + (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) - incl;
+    const uint64_t m2 = __ballot(ln < PB && ab2 < kk && ab2 + x >= kk);
+    if (!m2) return;
+    const int j = __builtin_ctzll(m2);
+    d = (uint32_t)(L * PB + j);
+    above = (uint32_t)__builtin_amdgcn_readlane((int)ab2, j);
+}
+
 struct EmitSmem {
-    uint32_t hist[H1];
+    alignas(16) uint32_t hist[H1];
     uint32_t pre[MAX_CHUNKS + 1];   // candidates of the chunks before chunk c
     uint32_t acnt[MAX_CHUNKS];      // per chunk: candidates above T
     uint32_t ecnt[MAX_CHUNKS];      // per chunk: candidates equal to T
     uint32_t wsum[4 * TW], found[2];   // (block_prefix_runs<NR> uses NR * TW)
     uint32_t base, take, eq;        // this workgroup's chunk
-    uint32_t ckey[NCL];             // the row's candidates (key, chunk) when more than
+    uint32_t thr;                   // T (slot-speculative path)
+    alignas(16) uint32_t hist2[H2]; // level 2 (slot-speculative path; read as uint4)
+    uint32_t ncn[SPEC_C], gtc[SPEC_C];   // per chunk: candidates, keys above bin d0 (same)
+    alignas(16) uint32_t ckey[NCL]; // the row's candidates (key, chunk) when more than
     uint16_t cchk[NCL];             // fit in registers
 };
 static_assert(MAX_CHUNKS <= 65536, "chunk ids are 16-bit");
@@ -329,6 +366,22 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
         }
     }
     const uint32_t d0 = info[0].d0, krem = info[0].krem;
+    // read set, at most SPEC_C chunks: P = SPEC_N / C (rounded down to a power of two, at
+    // most CS) slots
+    // of every chunk's candidate list, slot e & (P - 1) of chunk e / P for e = tid + i TB,
+    // loaded in this round trip before the counts are known (slots past a chunk's count are
+    // ignored below); used when no chunk has more than P candidates
+    const uint32_t *L = a.cand + (int64_t)row * C * CS;
+    const bool spec_try = !KEEP && C <= SPEC_C;
+    constexpr int CS_LOG = VPT == 4 ? 10 : 12;   // log2(CS): a chunk has CS slots
+    static_assert((1 << CS_LOG) == CS, "chunk size");
+    const int pl = spec_try ? min(31 - __builtin_clz((uint32_t)(SPEC_N / C)), CS_LOG) : 0, P = 1 << pl;
+    uint32_t spk[SPEC_N / TB];
+#pragma unroll
+    for (int i = 0; i < SPEC_N / TB; ++i) {
+        const int e = tid + i * TB;
+        spk[i] = spec_try && (e >> pl) < C ? L[(int64_t)(e >> pl) * CS + (e & (P - 1))] : 0u;
+    }
     uint32_t key[VPT];
     chunk_keys<VPT, KEEP>(a, row, c, key);
     if constexpr (KEEP) {
@@ -341,6 +394,84 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
             for (int i = tid; i < a.w; i += TB) wout[i] = (int64_t)(a.m + i);
         }
     }
+    bool spec = false;
+    if (spec_try) {
+        for (int i = tid; i < H1 / 4; i += TB) ((uint4 *)S.hist)[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = tid; i < H2; i += TB) S.hist2[i] = 0u;
+        if (tid < SPEC_C) {
+            S.acnt[tid] = 0u;
+            S.ecnt[tid] = 0u;
+        }
+        bool over = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ch = 4 * tid + i;
+            if (ch < C) {
+                S.ncn[ch] = nc[i];
+                S.gtc[ch] = gt[i];
+                over |= nc[i] > (uint32_t)P;
+            }
+        }
+        spec = !__syncthreads_or(over);
+    }
+    uint32_t thr = 0u;
+    if (spec) {
+        // every thread counts its valid slots (spk, 0 elsewhere: candidate keys are real
+        // keys, never 0) into the LDS histograms, level by level; one wave finds each digit
+        // by lane scans (its LDS operations complete in order) and, at the end, with lane =
+        // chunk, the T-equal keys taken in chunk order and the output bases
+#pragma unroll
+        for (int i = 0; i < SPEC_N / TB; ++i) {
+            const int e = tid + i * TB, ch = e >> pl;
+            spk[i] = ch < C && (uint32_t)(e & (P - 1)) < S.ncn[ch] ? spk[i] : 0u;
+            if (spk[i]) atomicAdd(&S.hist[(spk[i] >> S1) & (H1 - 1)], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            uint32_t d1, a1;
+            wave_find_digit<H1 / 64>(S.hist, krem, d1, a1);
+            if (tid == 0) {
+                S.found[0] = d1;
+                S.found[1] = krem - a1;
+            }
+        }
+        __syncthreads();
+        const uint32_t d1 = S.found[0], kr = S.found[1];
+#pragma unroll
+        for (int i = 0; i < SPEC_N / TB; ++i)
+            if (spk[i] && ((spk[i] >> S1) & (H1 - 1)) == d1) atomicAdd(&S.hist2[spk[i] & (H2 - 1)], 1u);
+        __syncthreads();
+        if (tid < 64) {
+            uint32_t d2, a2;
+            wave_find_digit<H2 / 64>(S.hist2, kr, d2, a2);
+            if (tid == 0) {
+                S.thr = (d0 << S0) | (d1 << S1) | d2;
+                S.take = kr - a2;   // (here: how many keys equal to T the row takes)
+            }
+        }
+        __syncthreads();
+        const uint32_t t = S.thr, need = S.take;
+#pragma unroll
+        for (int i = 0; i < SPEC_N / TB; ++i) {
+            const int ch = (tid + i * TB) >> pl;
+            if (spk[i] && spk[i] > t) atomicAdd(&S.acnt[ch], 1u);
+            else if (spk[i] && spk[i] == t) atomicAdd(&S.ecnt[ch], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            const int ln = tid;
+            const uint32_t ac = ln < C ? S.acnt[ln] : 0u, ec = ln < C ? S.ecnt[ln] : 0u;
+            const uint32_t ebefore = ma_wave_prefix_u32(ec) - ec;
+            const uint32_t take = need > ebefore ? min(need - ebefore, ec) : 0u;
+            const uint32_t sel = ln < C ? S.gtc[ln] + ac + take : 0u;
+            const uint32_t sbefore = ma_wave_prefix_u32(sel) - sel;
+            if (ln == c) {
+                S.base = sbefore;
+                S.take = take;
+                S.eq = ec;
+            }
+        }
+    } else {
     uint32_t run[1] = {nc[0] + nc[1] + nc[2] + nc[3]};
     const uint32_t NC = block_prefix_runs<1>(run, S.wsum);
     {
@@ -360,7 +491,6 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
     }
     __syncthreads();
     // candidate g of the row: chunk ch with pre[ch] <= g < pre[ch + 1], slot g - pre[ch]
-    const uint2 *L = a.cand + (int64_t)row * C * CS;
     auto locate = [&](uint32_t g) {
         int lo = 0, hi = C - 1;
         while (lo < hi) {
@@ -382,7 +512,7 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
             for (int i = 0; i < 8; ++i) {
                 const uint32_t g = g0 + tid + i * TB;
                 chs[i] = g < NC ? locate(g) : 0;
-                kx[i] = g < NC ? L[(int64_t)chs[i] * CS + (g - S.pre[chs[i]])].x : 0u;
+                kx[i] = g < NC ? L[(int64_t)chs[i] * CS + (g - S.pre[chs[i]])] : 0u;
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -403,7 +533,7 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
             cc[i] = 0u;
             if (g < NC) {
                 const int ch = locate(g);
-                ck[i] = L[(int64_t)ch * CS + (g - S.pre[ch])].x;
+                ck[i] = L[(int64_t)ch * CS + (g - S.pre[ch])];
                 cc[i] = (uint32_t)ch;
             }
         }
@@ -418,7 +548,7 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
         } else {
             for (uint32_t g = tid; g < NC; g += TB) {
                 const int ch = locate(g);
-                f(L[(int64_t)ch * CS + (g - S.pre[ch])].x, (uint32_t)ch);
+                f(L[(int64_t)ch * CS + (g - S.pre[ch])], (uint32_t)ch);
             }
         }
     };
@@ -442,7 +572,7 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
         if (((x >> S1) & (H1 - 1)) == d1) atomicAdd(&S.hist[x & (H2 - 1)], 1u);
     });
     __syncthreads();
-    uint32_t thr, need;
+    uint32_t need;
     {
         uint32_t cnt[1] = {S.hist[tid]};
         find_digit<1>(cnt, kr, S.wsum, S.found);
@@ -487,10 +617,12 @@ __global__ void __launch_bounds__(TB) topk_emit_kernel(TopkArgs a) {
             base += sel[i];
         }
     }
+    }
     // this workgroup's share of the row's histogram, cleared for the next call (the
     // boundary kernel, its only reader, has finished)
     for (int b = c * TB + tid; b < H0; b += C * TB) a.state[row].hist[b] = 0u;
     __syncthreads();
+    if (spec) thr = S.thr;
     const uint32_t cbase = S.base, ctake = S.take, ceq = S.eq;
     uint32_t selbits = 0;
     if (ctake == 0u || ctake >= ceq) {
@@ -575,7 +707,7 @@ extern "C" int64_t ma_topk_workspace_bytes(int rows, int n) {
     if (rows <= 0 || n <= 0 || !topk_vpt(n)) return 0;
     const int vpt = topk_vpt(n);
     const int64_t C = (n + TB * vpt - 1) / (TB * vpt);
-    return chunk_bytes(rows, n) + align256((int64_t)rows * C * TB * vpt * (int64_t)sizeof(uint2));
+    return chunk_bytes(rows, n) + align256((int64_t)rows * C * TB * vpt * (int64_t)sizeof(uint32_t));
 }
 
 namespace {
@@ -609,7 +741,7 @@ int topk_prepare(TopkArgs &a, int &vpt, const char *who, const float *rank, int6
     a.idx_stride = idx_stride;
     a.state = (RowState *)state;
     a.chunk = (ChunkInfo *)workspace;
-    a.cand = (uint2 *)((char *)workspace + chunk_bytes(rows, n));
+    a.cand = (uint32_t *)((char *)workspace + chunk_bytes(rows, n));
     return MA_OK;
 }
 
