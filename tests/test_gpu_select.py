@@ -84,3 +84,27 @@ def test_topk_workspace_reuse_and_unaligned(gpu):
         xg = base.to(gpu)[:rows, 1:n + 1]                     # 4-byte offset, row stride 40001
         got = topk_ascending(xg, k)
         assert torch.equal(got.cpu(), want), (rows, n, k, "view")
+
+
+@pytest.mark.parametrize("n,k", [(32768, 2048), (40000, 3000), (65536, 700)])
+def test_topk_ties_spread_over_chunks(gpu, n, k):
+    """Rows of at most 64 chunks whose boundary bin holds a few keys per chunk, so every
+    workgroup of the emit kernel reads its candidates speculatively: keys equal to the k-th
+    value in several chunks (ties taken in index order across chunks), in one chunk only,
+    and a row whose one chunk holds more boundary-bin keys than its speculative slots
+    (the emit kernel's general path for that row)."""
+    g = torch.Generator().manual_seed(n + k)
+    rows = 4
+    # values over ~20 octaves: a 13-bit bin (16 per octave) holds few keys, so the boundary
+    # bin has a few candidates per chunk
+    x = (torch.randn((rows, n), generator=g) * 3.0).exp()
+    kth = x.sort(dim=-1, descending=True).values[:, k - 1:k]
+    pos = torch.arange(n)
+    x[0, pos % 4099 == 17] = kth[0, 0]                # the k-th value repeated in every chunk
+    x[1, (pos >= 3000) & (pos < 3040)] = kth[1, 0]    # 40 copies inside one chunk
+    x[2, (pos >= 5000) & (pos < 5400)] = kth[2, 0] * (1 + 1e-6 * torch.arange(400) / 400)  # one dense chunk
+    got = topk_ascending(x.to(gpu), k)
+    assert torch.equal(got.cpu(), OS.topk_ascending(x, k))
+    mask = (torch.rand((rows, n), generator=g) > 0.02).to(torch.uint8)
+    got = topk_ascending(x.to(gpu), k, mask.to(gpu))
+    assert torch.equal(got.cpu(), OS.topk_ascending(x, k, mask))
