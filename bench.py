@@ -351,7 +351,7 @@ def main():
         del layers, result
         torch.cuda.empty_cache()
         line["extras"] = {"c1_block_step": extra_c1_block(a), "c3_keep_step": extra_c3_keep(a),
-                          "evict_28_layers": extra_evict(a)}
+                          "c4_block_step": extra_c4_block(a), "evict_28_layers": extra_evict(a)}
     if not a.no_cpu:
         from oracle import attention as OA
 
@@ -761,6 +761,96 @@ def extra_c3_keep(a, layers=4, reps=5):
                         f"{sh.keep_k} of {sh.n} per KV head, compaction in place + append of 32 tokens; "
                         f"{layers} layers, eager, median of {reps}",
             "us_per_layer_keep_step": round(sec * 1e6, 1), "roofline": _roof(nbytes, flops, sec)}
+
+
+def extra_c4_block(a, L=28, dense=2):
+    """BASELINE config 4, the ragged multi-sequence full-model block step: 8 sequences with
+    prefix lengths uniform in [8 192, 131 072] (seed 1234), 28 layers of the config-1 head
+    shape (the first 2 dense), packed int4 KV (every whole group quantized), read 2 048 /
+    keep 4 096 per KV head.  Per sequence, from its freshly built cache, one block: step 0
+    of every layer (fast-path routing: split-K attention, value-aware scores with the
+    fused read-set select, gather), the lookahead eviction (keep score, keep set, packed
+    lazy rebuild), 3 denoising sub-steps and the block's finalize (its KV appended)
+    (session.py:1403-1454, 1985-2034, 270-361, 1286-1336, 2289-2297).  Launched op by op
+    from Python as the session runs it; the sequences one after another.  Algorithmic
+    bytes per sequence of prefix n (P = n x 4 KV heads x 160 B of int4 K and V with their
+    scales): step 0 streams the prefix twice in a sparse layer (attention, scores) and once
+    in a dense one; the eviction reads V once per layer (keep score) and reads and writes
+    the 4 096 kept entries; the sub-steps read the 2 048-entry bf16 compact buffers of the
+    sparse layers and the 4 096 kept entries of the dense ones."""
+    from maskahead_amd.cache import PackedKVCache
+    from maskahead_amd.config import QuantizationConfig
+    from maskahead_amd.eviction import EvictionConfig, EvictionState
+    from maskahead_amd.runtime.fastpath import BlockContext, FastLayerPath
+    from maskahead_amd.runtime.session import live_slot_masks, lookahead_evict
+
+    dev = torch.device("cuda:0")
+    hq, hkv, d, t, read_k, keep_k, W = 28, 4, 128, 32, 2048, 4096, 64
+    lens = torch.randint(8192, 131073, (8,), generator=torch.Generator().manual_seed(1234)).tolist()
+    cfg = EvictionConfig(policy="lookahead", recent_window=W, capacity_floor=512, compaction="lazy",
+                         repack_below=1.0, sink_tokens=4)
+
+    def run(n, seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        chan = torch.empty((1, hkv, 1, d), device=dev).log_normal_(0.0, 0.5, generator=g)
+        k = torch.randn((1, hkv, n, d), device=dev, generator=g) * chan
+        k[:, :, :4] *= 8.0
+        k = k.to(torch.bfloat16)
+        v = torch.randn((1, hkv, n, d), device=dev, generator=g).to(torch.bfloat16)
+        blocks = [tuple(x.to(torch.bfloat16) for x in (
+            torch.randn((1, hq, t, d), device=dev, generator=g),
+            torch.randn((1, hkv, t, d), device=dev, generator=g) * chan,
+            torch.randn((1, hkv, t, d), device=dev, generator=g))) for _ in range(L)]
+        cache = PackedKVCache(num_layers=L, batch_size=1, num_kv_heads=hkv, head_dim=d, max_tokens=n + 4 * t,
+                              quant=QuantizationConfig(residual_tokens=0), device=dev)
+        cache.begin_append(n)
+        for layer in range(L):
+            cache.stage_layer(layer, torch.roll(k, 977 * layer, dims=2), v)
+        cache.commit_append()
+        del k, v
+        st = EvictionState(num_layers=L, batch_size=1, num_kv_heads=hkv, capacity=n + 4 * t, device=dev)
+        st.append(range(n))
+        fp = FastLayerPath(cache=cache, block_size=t, query_indices=list(range(t)), dense_prefix_layers=dense)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ctx = BlockContext(step_index=0, old_cache_len=n, topk=read_k, evicting=True, live_len=st.live,
+                           want_mass=True, live_slots={layer: st.phys[layer, ..., :st.live] for layer in range(L)})
+        for layer in range(L):
+            fp.route(layer, *blocks[layer], ctx)
+        lookahead_evict(cache, st, cfg, keep_k, fp.last_mass, None, next_position=n)
+        fp.slot_masks = live_slot_masks(cache, st)
+        for step in (1, 2, 3):
+            ctx.step_index = step
+            for layer in range(L):
+                fp.route(layer, *blocks[layer], ctx)
+        cache.begin_append(t)
+        for layer in range(L):
+            cache.stage_layer(layer, blocks[layer][1], blocks[layer][2])
+        cache.commit_append()
+        st.append(range(n, n + t))
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+        del cache, st, fp, blocks
+        torch.cuda.empty_cache()
+        return sec
+
+    run(8192, 999)                                        # warm-up: kernels loaded, allocator grown
+    secs = [run(n, 1234 + i) for i, n in enumerate(lens)]
+    r = (hq // hkv) * t
+    nbytes = flops = 0
+    for n in lens:
+        P = n * hkv * 160
+        nbytes += (L - dense) * 2 * P + dense * P                                     # step 0
+        nbytes += L * n * hkv * 80 + 2 * L * keep_k * hkv * 160                       # eviction
+        nbytes += 3 * ((L - dense) * read_k * hkv * d * 2 * 2 + dense * keep_k * hkv * 160)   # sub-steps
+        flops += (L - dense) * 6 * r * n * d * hkv + dense * 4 * r * n * d * hkv
+        flops += 3 * ((L - dense) * 4 * r * read_k * d * hkv + dense * 4 * r * keep_k * d * hkv)
+    sec = sum(secs)
+    return {"workload": f"c4: 8 sequences, prefixes {sorted(lens)}, 28 layers ({dense} dense), packed int4, "
+                        f"read {read_k} / keep {keep_k}: step 0 + lookahead eviction + 3 sub-steps + finalize per "
+                        f"sequence, eager, sequences one after another",
+            "us_per_block_step": round(sec * 1e6, 1),
+            "us_per_sequence": [round(x * 1e6, 1) for x in secs], "roofline": _roof(nbytes, flops, sec)}
 
 
 def extra_evict(a):

@@ -145,12 +145,21 @@ def selector_topk(query, view, *, query_indices, topk, current_key=None, domain=
 
 def gather_packed_kv(view, indices, *, dtype=torch.bfloat16, backend="auto", out_key=None, out_value=None):
     """Selected entries of a cache view, dequantized, as [B, Hkv, k, D] K and V
-    (ops.py:570-662, 835-855).  Indices outside the view produce zeros."""
+    (ops.py:570-662, 835-855).  Indices outside the view produce zeros.  ``view`` may also
+    be the view's Prefix (its mask is not used)."""
     if indices.ndim != 3:
         raise ValueError("indices must have shape [B,Hkv,K]")
     _choose_backend(backend, indices)
     b, hkv, k = indices.shape
-    d = _view_head_dim(view, out_key=out_key, out_value=out_value)
+    if isinstance(view, Prefix):
+        prefix = view
+        src = prefix.kq if prefix.nq else prefix.kf
+        d = int(src.shape[-2] if prefix.nq else src.shape[-1])
+        if out_key is not None and int(out_key.shape[-1]) != d:
+            raise ValueError("output head_dim differs from the prefix's")
+    else:
+        d = _view_head_dim(view, out_key=out_key, out_value=out_value)
+        prefix = Prefix.from_view(view)
     if out_key is None:
         out_key = torch.empty((b, hkv, k, d), device=indices.device, dtype=dtype)
     if out_value is None:
@@ -160,7 +169,6 @@ def gather_packed_kv(view, indices, *, dtype=torch.bfloat16, backend="auto", out
     idx = indices if indices.dtype == torch.int64 else indices.to(torch.int64)
     if idx.stride(-1) != 1:
         idx = idx.contiguous()
-    prefix = Prefix.from_view(view)
     prefix.check_mask(b, hkv)
     lib = N.load()
     rc = lib.ma_gather_kv(prefix.native(), b, hkv, d, idx.data_ptr(), N.i64arr(idx.stride(0), idx.stride(1)), k,

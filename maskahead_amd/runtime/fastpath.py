@@ -114,15 +114,30 @@ class FastLayerPath:
     chunk_mass: dict = field(default_factory=dict)
     qprobe_mass: dict = field(default_factory=dict)
     _rows_cache: tuple | None = None
+    _prefix_cache: dict = field(default_factory=dict)
+    _compact_prefix: dict = field(default_factory=dict)
 
     @property
     def head_dim(self) -> int:
         return self.cache.head_dim
 
     def prefix(self, layer_idx: int) -> Prefix:
-        """session.py:1362-1367."""
-        pre = Prefix.from_view(self.cache.layer_view(layer_idx))
-        pre.mask = self.slot_masks.get(layer_idx)
+        """session.py:1362-1367.  Kept per layer while the cache's planes (storage and
+        strides), its lengths and the layer's slot mask are the ones it was built from: the
+        descriptor holds nothing else, so a cache that grew, compacted, rebuilt or appended
+        gives a new one (building the view and descriptor is most of a step's host time)."""
+        c = self.cache
+        mask = self.slot_masks.get(layer_idx)
+        key = (c.length, c.quantized_length, c.residual_length, id(mask),
+               tuple((t.data_ptr(), t.stride()) if t is not None else None
+                     for t in (c.k_q, c.k_scale, c.k_zero, c.v_q, c.v_scale, c.v_zero, c.k_residual, c.v_residual,
+                               c.k_fp, c.v_fp)))
+        hit = self._prefix_cache.get(layer_idx)
+        if hit is not None and hit[0] == key and hit[2] is mask:
+            return hit[1]
+        pre = Prefix.from_view(c.layer_view(layer_idx))
+        pre.mask = mask
+        self._prefix_cache[layer_idx] = (key, pre, mask)
         return pre
 
     def rows(self, positions):
@@ -240,7 +255,7 @@ class FastLayerPath:
             self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
         if need_sel:
             state = self.ensure_state(layer_idx, k)
-            gather_packed_kv(self.cache.layer_view(layer_idx), idx, dtype=self.compute_dtype,
+            gather_packed_kv(prefix, idx, dtype=self.compute_dtype,
                              out_key=state.key[:, :, :k, :], out_value=state.value[:, :, :k, :])
             state.indices = idx
             state.selected_k = k
@@ -258,7 +273,13 @@ class FastLayerPath:
         if k + ncur > state.key.shape[2]:
             raise RuntimeError("compact cache buffer capacity exceeded")
         cd = self.compute_dtype
-        pre = Prefix.dense(state.key[:, :, :k, :], state.value[:, :, :k, :])
+        key = (k, state.key.data_ptr(), state.value.data_ptr(), state.key.stride(), state.value.stride())
+        hit = self._compact_prefix.get(layer_idx)
+        if hit is not None and hit[0] == key:
+            pre = hit[1]   # the same compact buffer, length and strides: the same descriptor
+        else:
+            pre = Prefix.dense(state.key[:, :, :k, :], state.value[:, :, :k, :])
+            self._compact_prefix[layer_idx] = (key, pre)
         out, _ = splitk_attention(query.to(cd), pre, current_key.to(cd), current_value.to(cd),
                                   scaling=self.head_dim ** -0.5)
         return out.to(query.dtype)
