@@ -194,6 +194,7 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
     # the reference unpacks such a prefix to query.dtype and reads that copy from here on
     # (splitk.py:513-516); the statistics carry a copy that says so
     used = prefix
+    nat = prefix.native()   # built before the copy below, which then shares it
     if prefix.nq and (r > dequant_rows or prefix.n > packed_direct_max) and query.dtype != torch.float32:
         used = prefix.with_vround(N.dtype_code(query.dtype))
     dev = query.device
@@ -213,7 +214,7 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
     ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
     tc = current_key.shape[2]
     rc = lib.ma_splitk_attention(
-        N.t4(query), b, hq, t, d, prefix.native(), hkv, N.t4(current_key if tc else None),
+        N.t4(query), b, hq, t, d, nat, hkv, N.t4(current_key if tc else None),
         N.t4(current_value if tc else None), tc, int(causal_block), int(q_pos0), int(c_pos0), scale,
         N.t4(out), N.ptr(mp), N.ptr(lp), N.ptr(op), int(split_tokens), ws.data_ptr(), ws_bytes,
         N.stream_of(query))
