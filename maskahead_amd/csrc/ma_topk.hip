@@ -13,13 +13,16 @@
 // in all three kernels, so a chunk is re-read from the L2 of the XCD that read it first.
 // Elements are monotone 32-bit keys (larger float -> larger key, -0.0 == +0.0, NaN above
 // +inf, dead slots -inf); the k-th largest key T is found digit by digit, 13 + 11 + 8 bits:
-//   1. hist:     every chunk adds its 13-bit histogram into the row's global histogram.
+//   1. hist:     every chunk adds its 13-bit histogram into the row's global histogram
+//                (skipped when the score pass has built it: ma_topk_select_hist_ready).
 //   2. boundary: every workgroup reads the row's histogram and finds the bin d0 holding
 //                the k-th key and how many keys of that bin are still to take (krem);
-//                it counts its chunk's keys above bin d0 and writes the keys of bin d0
-//                (key, index) to the chunk's candidate slots.
+//                it counts its chunk's keys above bin d0 and writes the keys of bin d0 to
+//                the chunk's candidate slots, in index order.
 //   3. emit:     every workgroup reads the row's candidates (typically about 1% of the
-//                row) and finds the remaining 19 bits of T (two LDS histograms), the
+//                row; for rows of at most SPEC_C chunks a fixed number of slots of every
+//                chunk, loaded before the counts are known, when none overflows) and
+//                finds the remaining 19 bits of T (two LDS histograms), the
 //                number `need` of keys equal to T that are selected (the first `need` in
 //                index order) and, from all chunks' counts, its own output base and how
 //                many of its T-equal keys it takes; then it writes its selected indices,
