@@ -87,3 +87,19 @@ def test_rebuild_arguments_are_checked_on_the_host(lib):
     rc = lib.ma_rebuild_packed(old, 1, 1, 64, new, None, 0, 1, None, 0, 0, None, 0, 0, None, 0, 0, None, 0,
                                None, 0, 0, None, None)   # one kept group, but new storage of 0 entries
     assert rc == N.MA_EINVAL and b"expected" in lib.ma_last_error()
+
+
+def test_fused_score_select_arguments_are_checked_on_the_host(lib):
+    """The score pass with the select's first histogram level and the select that uses it
+    reject bad arguments before any launch; the Python pair rejects a bad rank."""
+    rc = lib.ma_prefix_scores_hist(N.MaTensor4(), 1, 28, 32, 128, N.MaPrefix(), 4, None, 32, None, None, None, 0,
+                                   1.0, 1, 0, None, None, 3, None, 0, None)
+    assert rc == N.MA_EINVAL and b"rank must be" in lib.ma_last_error()
+    rc = lib.ma_topk_select_hist_ready(None, 0, None, 0, -1, 10, 1, None, 1, None, None, 0, None, 0, None)
+    assert rc == N.MA_EINVAL and b"bad arguments" in lib.ma_last_error()
+    from maskahead_amd.kernels import prefix_scores_topk
+
+    with pytest.raises(ValueError):
+        prefix_scores_topk(None, None, (None, None, None, None), [0], 1, value=False, rank="score")
+    with pytest.raises(ValueError):
+        prefix_scores_topk(None, None, (None, None, None, None), [0], 1, value=True, rank="keys")
