@@ -264,10 +264,11 @@ def main():
     # GQA-reduced VALU variant and the padded 32-row MFMA variant, each forced
     variants = {}
     for pos in ([sh.t - 1], [sh.t - 2, sh.t - 1]):
+        pos_dev = torch.tensor(pos, dtype=torch.int32, device=dev)   # a device row table, made before capture
         for name, mode in (("valu", 2), ("mfma", 1)):
             prev_path = lib.ma_prefix_scores_path(mode)
             try:
-                variants[(len(pos), name)] = time_graph(lambda: scores_all(pos), a.steps, a.warmup)[0] / a.layers
+                variants[(len(pos), name)] = time_graph(lambda: scores_all(pos_dev), a.steps, a.warmup)[0] / a.layers
             finally:
                 lib.ma_prefix_scores_path(prev_path)
     del stats_all

@@ -78,6 +78,24 @@ class LayerCacheView:
     k_chan: torch.Tensor | None = None
 
 
+def _dynamic_layer(dyn, layer: int):
+    """(K, V) of one layer of a prefill cache object, through the first access it offers
+    (the transformers cache APIs: tuple indexing; key_cache / value_cache lists; 5.x
+    layers[i].keys / .values); TypeError when none yields both tensors."""
+    kv = None
+    try:
+        k, v = dyn[layer]
+        kv = (k, v)
+    except Exception:
+        if hasattr(dyn, "key_cache"):
+            kv = (dyn.key_cache[layer], dyn.value_cache[layer])
+        elif hasattr(dyn, "layers"):
+            kv = (dyn.layers[layer].keys, dyn.layers[layer].values)
+    if kv is None or kv[0] is None or kv[1] is None:
+        raise TypeError(f"cannot read layer {layer} out of {type(dyn).__name__}")
+    return kv
+
+
 def _ceil_to(x: int, m: int) -> int:
     return -(-x // m) * m
 
@@ -118,6 +136,9 @@ class PackedKVCache:
         self.peak_used_bytes = self.peak_allocated_bytes = 0
         self.memory_trace: list[list[int]] | None = None
         self._append_plan: AppendPlan | None = None
+        # bumped whenever the planes are replaced (growth, shrink after compaction): holders
+        # of views or descriptors of the planes drop them when it changes
+        self.planes_generation = 0
         for name in _UNITS:
             setattr(self, name, None)
         gk = quant.key_token_group
@@ -172,6 +193,7 @@ class PackedKVCache:
             if keep:
                 new[:, :, :, :keep].copy_(old[:, :, :, :keep])
             setattr(self, name, new)
+        self.planes_generation += 1
 
     @property
     def capacity(self) -> int:
@@ -306,6 +328,31 @@ class PackedKVCache:
             assert self.quantized_length + self.residual_length == self.length, "cache length invariant failed"
         self._append_plan = None
         self._note_peak()
+
+    def load_dynamic_cache(self, dynamic_cache) -> None:
+        """Fill an empty cache with a prefill's per-layer K / V (the reference's
+        load_dynamic_cache, cache.py:568-606): one append of get_seq_length() tokens, each
+        layer staged through the HIP append and quantizers; any failure aborts the append.
+        A layer is read by whichever access the object offers: ``cache[i]`` -> (K, V), the
+        ``key_cache`` / ``value_cache`` lists, or ``layers[i].keys`` / ``.values``."""
+        if self.length != 0 or self._append_plan is not None:
+            raise RuntimeError("load_dynamic_cache requires an empty cache")
+        if dynamic_cache is None:
+            return
+        n = int(dynamic_cache.get_seq_length())
+        if n == 0:
+            return
+        if n > self.max_tokens:
+            raise RuntimeError(f"prefill cache length {n} exceeds capacity {self.max_tokens}")
+        self.begin_append(n)
+        try:
+            for layer in range(self.num_layers):
+                key, value = _dynamic_layer(dynamic_cache, layer)
+                self.stage_layer(layer, key[..., :n, :].contiguous(), value[..., :n, :].contiguous())
+            self.commit_append()
+        except BaseException:
+            self.abort_append()
+            raise
 
     # -- views ----------------------------------------------------------------------------
     def layer_view(self, layer_idx: int) -> LayerCacheView:

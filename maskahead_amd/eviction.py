@@ -136,6 +136,11 @@ class EvictionState:
         self._cols: dict[str, torch.Tensor] = {}
         self.live = 0
         self.pin: tuple[int | torch.Tensor, int] | None = None
+        # sink statistic of the evictions (eviction.py:446-451): lanes that dropped one of
+        # positions 0..3, counted on the device (read back only when asked for), and lanes
+        # evicted in all
+        self._sink_drops: torch.Tensor | None = None
+        self.lanes_evictions = 0
         self._ensure(max(int(capacity), 1))
 
     # the columns, as attributes (views of the whole storage; rows >= live are unused)
@@ -143,6 +148,17 @@ class EvictionState:
     n = property(lambda self: self._cols["n"])
     pos = property(lambda self: self._cols["pos"])
     phys = property(lambda self: self._cols["phys"])
+
+    @property
+    def sink_lanes_evicted(self) -> int:
+        """(layer, batch, KV head) lane evictions so far that dropped a position < 4."""
+        return 0 if self._sink_drops is None else int(self._sink_drops.item())
+
+    def state_nbytes(self) -> int:
+        """Bytes of the policy's own per-entry state -- the EMA, its observation count and
+        the position of every live entry of every lane (eviction.py:460-466)."""
+        per_entry = sum(self._cols[name].element_size() for name in ("g", "n", "pos"))
+        return self.num_layers * self.batch_size * self.num_kv_heads * self.live * per_entry
 
     @property
     def rows(self) -> int:
@@ -290,5 +306,39 @@ class EvictionState:
                 raise ValueError(f"policy {cfg.policy} needs a score_fn")
             score = score_fn(capacity) if cfg.policy == "greedy_set" else score_fn()
         keep = self.survivors(cfg, capacity, spread, score)
+        self._count_sink_drops(keep)
         self.compact(keep)
         return keep
+
+    def _count_sink_drops(self, keep: torch.Tensor) -> None:
+        """Add the lanes whose keep set drops one of positions 0..3 (before compact)."""
+        sinks = self._in_use("pos") < 4
+        kept = torch.gather(sinks, -1, keep).sum(-1)
+        drops = (kept < sinks.sum(-1)).sum()
+        self._sink_drops = drops if self._sink_drops is None else self._sink_drops + drops
+        self.lanes_evictions += int(sinks[..., 0].numel())
+
+
+def live_cache_nbytes(pos: torch.Tensor, *, live: int, head_dim: int, k_bits: int, v_bits: int,
+                      key_token_group: int, value_channel_group: int, param_bytes: int = 2,
+                      compute_bytes: int = 2) -> int:
+    """Bytes a cache holding exactly the live set pos[..., :live] would occupy
+    (eviction.py:468-516): the packed or 16-bit payload of every live entry; for packed
+    keys one scale/zero vector per key group that still holds a live entry (a group lives
+    while any of its entries does), for packed values one per entry and value group.
+    pos: [L, B, Hkv, rows] positions, the first `live` of each lane valid, any order."""
+    if live <= 0:
+        return 0
+    lanes = pos.shape[0] * pos.shape[1] * pos.shape[2]
+    entries = lanes * live
+    if k_bits >= 16:
+        k_bytes = entries * head_dim * compute_bytes
+    else:
+        grp = torch.sort(pos[..., :live].reshape(lanes, live) // key_token_group, dim=-1).values
+        groups = lanes + int((grp[:, 1:] != grp[:, :-1]).sum())      # distinct groups per lane, summed
+        k_bytes = entries * head_dim * k_bits // 8 + groups * head_dim * 2 * param_bytes
+    if v_bits >= 16:
+        v_bytes = entries * head_dim * compute_bytes
+    else:
+        v_bytes = entries * head_dim * v_bits // 8 + entries * (head_dim // value_channel_group) * 2 * param_bytes
+    return k_bytes + v_bytes

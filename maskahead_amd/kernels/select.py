@@ -20,18 +20,24 @@ from .. import _native as N
 from .splitk import prefix_scores   # (splitk does not import this module)
 
 _STATES: dict = {}
+_MAX_STATES = 8
 
 
 def _state(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """The zero-initialised select state of (`device`, its current stream -- `stream` when
-    the caller has it), at least nbytes."""
+    the caller has it), at least nbytes.  At most _MAX_STATES are kept (least recently
+    used dropped first), so streams that come and go do not accumulate states; a state is
+    only ever used on the stream it was allocated on, so dropping it hands the memory back
+    to the caching allocator in that stream's order."""
     key = (device.index, stream if stream is not None else torch.cuda.current_stream(device).cuda_stream)
-    st = _STATES.get(key)
+    st = _STATES.pop(key, None)
     if st is None or st.numel() < nbytes:
         # allocated and zero-filled on the current stream; the old one goes back to the
         # caching allocator, which reuses it in that stream's order
         st = torch.zeros((nbytes,), device=device, dtype=torch.uint8)
-        _STATES[key] = st
+    _STATES[key] = st                              # most recently used last
+    while len(_STATES) > _MAX_STATES:
+        _STATES.pop(next(iter(_STATES)))
     return st
 
 

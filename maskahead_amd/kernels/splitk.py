@@ -222,13 +222,36 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
     return out, ((mp, lp, op, used) if want_prefix else None)
 
 
+_ROW_TABLES: dict = {}
+
+
+def _row_table(rows: tuple, device: torch.device) -> torch.Tensor:
+    """The int32 device copy of a host list of selection rows, made once per (device, list)
+    by a synchronous copy and kept, so that a call under HIP graph capture finds it
+    resident: a copy recorded during capture would read its host source again at every
+    replay, after that temporary was freed.  Raises under capture for a list not seen
+    before (pass the rows as a device tensor there)."""
+    key = (device.index, rows)
+    t = _ROW_TABLES.get(key)
+    if t is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("q_rows given as a host list that was not used before graph capture: pass an int32 "
+                             "device tensor, or make one call with these rows before capturing")
+        if len(_ROW_TABLES) >= 64:
+            _ROW_TABLES.pop(next(iter(_ROW_TABLES)))
+        t = torch.tensor(rows, dtype=torch.int32, device=device)
+        _ROW_TABLES[key] = t
+    return t
+
+
 def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: bool, scaling=None,
                   block_m: int = 64, block_n: int = 64, _topk_hist=None):
     """Per prefix entry: mass a_j (mean prefix-softmax over the selection rows) and, with
     value=True, a_j * ||v_j - c|| with c the mean of O_p over those rows
     (splitk.py:582-614).  q_rows: block positions of the selection queries -- an int
     tensor (on the GPU: used as given) or a host sequence / CPU tensor (checked; the whole
-    block in order takes the kernels' row-table-free path).
+    block in order takes the kernels' row-table-free path; any other host list is copied
+    to the device once and kept, see _row_table).
     Returns (mass, score) as [B, Hkv, n] f32 (score None when value=False); dead slots 0.
     _topk_hist = (rank, state): also build the read-set top-k's first-level histogram of the
     mass (rank 1) or score (rank 2) into that select state (select.prefix_scores_topk pairs
@@ -243,11 +266,10 @@ def prefix_scores(query, prefix: Prefix, stats, q_rows: torch.Tensor, *, value: 
     # host-side rows (a sequence, or a CPU tensor) are checked here; 0 .. T2-1 in order
     # needs no row table at all (mode "all"); device rows are clamped into the block in-kernel
     if not isinstance(q_rows, torch.Tensor) or not q_rows.is_cuda:
-        host = [int(x) for x in (q_rows.tolist() if isinstance(q_rows, torch.Tensor) else q_rows)]
+        host = tuple(int(x) for x in (q_rows.tolist() if isinstance(q_rows, torch.Tensor) else q_rows))
         if any(x < 0 or x >= t for x in host):
             raise ValueError(f"q_rows must be block positions in [0, {t})")
-        q_rows = None if host == list(range(len(host))) else \
-            torch.tensor(host, dtype=torch.int32).to(query.device, non_blocking=True)
+        q_rows = None if host == tuple(range(len(host))) else _row_table(host, query.device)
         t2 = len(host)
     else:
         q_rows = q_rows.to(dtype=torch.int32).contiguous()

@@ -116,6 +116,7 @@ class FastLayerPath:
     _rows_cache: tuple | None = None
     _prefix_cache: dict = field(default_factory=dict)
     _compact_prefix: dict = field(default_factory=dict)
+    _planes_generation: int = -1
 
     @property
     def head_dim(self) -> int:
@@ -125,8 +126,14 @@ class FastLayerPath:
         """session.py:1362-1367.  Kept per layer while the cache's planes (storage and
         strides), its lengths and the layer's slot mask are the ones it was built from: the
         descriptor holds nothing else, so a cache that grew, compacted, rebuilt or appended
-        gives a new one (building the view and descriptor is most of a step's host time)."""
+        gives a new one (building the view and descriptor is most of a step's host time).
+        When the cache has replaced its planes (planes_generation), every layer's kept
+        descriptor is dropped at once, so none keeps the old planes alive."""
         c = self.cache
+        gen = getattr(c, "planes_generation", 0)
+        if gen != self._planes_generation:
+            self._prefix_cache.clear()
+            self._planes_generation = gen
         mask = self.slot_masks.get(layer_idx)
         key = (c.length, c.quantized_length, c.residual_length, id(mask),
                tuple((t.data_ptr(), t.stride()) if t is not None else None
@@ -148,7 +155,7 @@ class FastLayerPath:
         if key == tuple(range(len(key))):
             return list(key)
         if self._rows_cache is None or self._rows_cache[0] != key:
-            t = torch.tensor(key, dtype=torch.int32).to(self.cache.device, non_blocking=True)
+            t = torch.tensor(key, dtype=torch.int32, device=self.cache.device)   # synchronous, kept
             self._rows_cache = (key, t)
         return self._rows_cache[1]
 

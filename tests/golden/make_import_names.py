@@ -1,9 +1,16 @@
-"""Write tests/golden/reference_kernel_imports.json: every name the reference package
-imports from its kernel-op modules (maskahead.kernels.ops, maskahead.kernels.splitk),
-with the file:line of each import, so that a CPU test can check that maskahead_amd
-provides the same names (the drop-in boundary).
+"""Write tests/golden/reference_kernel_imports.json, the drop-in boundary by name:
 
-The reference's source files are parsed as text with `ast` (nothing of the reference is
+* "names": every name the reference package imports from the modules this package
+  replaces (maskahead.kernels.ops, maskahead.kernels.splitk, maskahead.cache,
+  maskahead.eviction), with the file:line of each import;
+* "attributes": every attribute the reference's runtime modules (runtime/*.py) read or
+  call on a KV-cache object (``self.cache``, a local ``cache``, or a name bound to one)
+  or an eviction-state object (``self._eviction`` or a name bound to it), including
+  ``getattr(obj, "name", ...)`` reads, with file:line; attributes only ever assigned are
+  listed under "assigned".
+
+So a CPU test can check that maskahead_amd provides the same names and members.  The
+reference's source files are parsed as text with `ast` (nothing of the reference is
 imported or run).  Run in a container that has /root/reference:
 
     python tests/golden/make_import_names.py [/root/reference/src/maskahead]
@@ -16,7 +23,12 @@ import json
 import sys
 from pathlib import Path
 
-MODULES = {"kernels.ops": "ops", "kernels.splitk": "splitk"}
+MODULES = {"kernels.ops": "ops", "kernels.splitk": "splitk", "cache": "cache", "eviction": "eviction"}
+# receivers, by kind: attribute chains on `self` and local names
+SELF_ATTRS = {"cache": "cache", "_eviction": "eviction_state"}
+LOCAL_NAMES = {"cache": "cache"}
+# functions whose local `cache` is not a KV-cache object of this path
+NOT_KV_CACHE = {"dynamic_cache_nbytes"}   # runtime/generation_utils.py: a transformers DynamicCache
 
 
 def resolve(pkg_parts: list[str], node: ast.ImportFrom) -> str | None:
@@ -27,6 +39,42 @@ def resolve(pkg_parts: list[str], node: ast.ImportFrom) -> str | None:
     base = pkg_parts[:len(pkg_parts) - (node.level - 1)] if node.level > 1 else pkg_parts
     parts = base + ([node.module] if node.module else [])
     return ".".join(p for p in parts if p)
+
+
+def receiver_kind(node: ast.AST, bound: dict[str, str]) -> str | None:
+    """'cache' / 'eviction_state' when `node` is such an object's expression."""
+    if isinstance(node, ast.Attribute) and isinstance(node.value, ast.Name) and node.value.id == "self":
+        return SELF_ATTRS.get(node.attr)
+    if isinstance(node, ast.Name):
+        return bound.get(node.id, LOCAL_NAMES.get(node.id))
+    return None
+
+
+def scan_attributes(path: Path, rel: str, reads: dict, writes: dict) -> None:
+    tree = ast.parse(path.read_text(), filename=str(path))
+    for fn in ast.walk(tree):
+        if not isinstance(fn, (ast.FunctionDef, ast.AsyncFunctionDef)) or fn.name in NOT_KV_CACHE:
+            continue
+        # names bound in this function to a receiver (st = self._eviction)
+        bound: dict[str, str] = {}
+        for node in ast.walk(fn):
+            if isinstance(node, ast.Assign) and len(node.targets) == 1 and isinstance(node.targets[0], ast.Name):
+                kind = receiver_kind(node.value, {})
+                if kind:
+                    bound[node.targets[0].id] = kind
+        for node in ast.walk(fn):
+            if isinstance(node, ast.Attribute):
+                kind = receiver_kind(node.value, bound)
+                if kind:
+                    dst = writes if isinstance(node.ctx, ast.Store) else reads
+                    dst[kind].setdefault(node.attr, []).append(f"src/maskahead/{rel}:{node.lineno}")
+            elif isinstance(node, ast.Call) and isinstance(node.func, ast.Name) and node.func.id in ("getattr",
+                                                                                                  "hasattr"):
+                if len(node.args) >= 2 and isinstance(node.args[1], ast.Constant) and \
+                        isinstance(node.args[1].value, str):
+                    kind = receiver_kind(node.args[0], bound)
+                    if kind:
+                        reads[kind].setdefault(node.args[1].value, []).append(f"src/maskahead/{rel}:{node.lineno}")
 
 
 def main(root: Path) -> dict:
@@ -44,8 +92,15 @@ def main(root: Path) -> dict:
                 continue
             for alias in node.names:
                 out[short].setdefault(alias.name, []).append(f"src/maskahead/{rel.as_posix()}:{node.lineno}")
+    reads: dict = {"cache": {}, "eviction_state": {}}
+    writes: dict = {"cache": {}, "eviction_state": {}}
+    for path in sorted((root / "runtime").glob("*.py")):
+        scan_attributes(path, path.relative_to(root).as_posix(), reads, writes)
+    assigned = {k: {a: w for a, w in v.items() if a not in reads[k]} for k, v in writes.items()}
     return {"modules": {f"maskahead.{m}": s for m, s in MODULES.items()},
-            "names": {s: dict(sorted(v.items())) for s, v in out.items()}}
+            "names": {s: dict(sorted(v.items())) for s, v in out.items()},
+            "attributes": {k: dict(sorted(v.items())) for k, v in reads.items()},
+            "assigned": {k: dict(sorted(v.items())) for k, v in assigned.items()}}
 
 
 if __name__ == "__main__":
@@ -53,4 +108,5 @@ if __name__ == "__main__":
     data = main(src)
     dst = Path(__file__).resolve().parent / "reference_kernel_imports.json"
     dst.write_text(json.dumps(data, indent=1) + "\n")
-    print(f"{dst}: " + ", ".join(f"{s}: {len(v)} names" for s, v in data["names"].items()))
+    print(f"{dst}: " + ", ".join(f"{s}: {len(v)} names" for s, v in data["names"].items()) + "; "
+          + ", ".join(f"{k}: {len(v)} attributes" for k, v in data["attributes"].items()))
