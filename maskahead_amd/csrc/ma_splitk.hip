@@ -2,23 +2,18 @@
 // of a KV head's GQA group (the reference's splitk_attention, splitk.py:493-579).
 //
 // Pass 1 (splitk_fwd_kernel): one workgroup = one (batch, KV head) lane x one token range
-// (a prefix split, or the current block) x up to 7 row tiles of 32 query rows; 16 waves
-// with fixed roles, software-pipelined over 64-token tiles with one barrier per tile:
-//   S waves 0..6     S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
-//                    B = Q^T held in registers), so a lane owns ONE query row and 16
-//                    tokens of each 32-token half; online softmax with a lazily raised
-//                    reference max; the probabilities P^T (bf16) go to LDS exactly in the
-//                    register order the PV MFMA consumes, plus a per-row rescale factor.
-//   O waves 8..14    one tile behind: O^T = alpha * O^T + V^T P^T (A = V^T from LDS,
-//                    B = P^T from LDS); the accumulator keeps the lane's row.
-//   waves 7..14      staging: K lanes (waves 7..10) dequantize tile i+1 into the K buffer
-//                    and prefetch tile i+2; V lanes (waves 11..14) dequantize tile i into
-//                    the V buffer and prefetch tile i+1 (V is consumed one iteration later
-//                    than K).  A wave holds lanes of one role only, so no wave executes
-//                    both staging paths.
-// K, V and P are double-buffered; every wave holds at most ~128 VGPRs, so the 16 waves
-// fit 4 per SIMD and the MFMA work of one wave overlaps the VALU work of the others.
+// (a prefix split, or the current block) x up to 7 row tiles of 32 query rows; 8 waves of
+// up to 256 VGPRs, software-pipelined over 64-token tiles with one barrier per tile:
+//   waves 0..6   one row tile each.  S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = K rows
+//                from LDS, B = Q^T held in registers), so a lane owns ONE query row and 16
+//                tokens of each 32-token half; online softmax with a lazily raised
+//                reference max; O^T = alpha * O^T + V^T P^T with P^T straight from the
+//                softmax's registers (A = V^T from LDS).  The S^T MFMAs of tile i+1 are
+//                issued interleaved with the exp2 work of tile i.
+//   all waves    staging: threads 0..255 dequantize K items, 256..511 V items of tile i+2
+//                into the third K / V buffer, then issue the loads of tile i+3.
 // Pass 2 (splitk_combine_kernel): log-sum-exp merge of the partials into the output and
+// the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
 // the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
 #include <mutex>
 #include <type_traits>
@@ -29,10 +24,7 @@ using namespace ma;
 
 namespace {
 
-constexpr int NTH = 1024;
-constexpr int MAXS = 7;                     // row tiles (S/O wave pairs) per workgroup
-constexpr int NSTAGE = 8 * 64;              // staging lanes: waves 7..14 (wave 15 stages nothing)
-constexpr int KLANES = NSTAGE / 2;          // K lanes (waves 7..10), then as many V lanes (11..14)
+constexpr int MAXS = 7;                     // row tiles (compute waves) per workgroup
 // a row's running reference max is raised only when a tile's max exceeds it by more than
 // 2^8 in exp2 units, so most tiles skip the accumulator rescale; p <= 2^8 stays exact
 constexpr float LAZY_LOG2 = 8.0f;
@@ -53,19 +45,6 @@ struct FwdArgs {
     float *wm, *wl, *wsc;
     _Float16 *wo;
 };
-
-template <int D>
-struct FwdSmem {
-    KTileL<D> kt[2];
-    VTileL<D> vt[2];
-    uint4 p[2][MAXS][4][64];   // P^T fragments: [buffer][S wave][16-token chunk][lane]
-    float alpha[2][MAXS][32];  // rescale factor of each row, when resc is set
-    int resc[2][MAXS];
-    uint64_t kmask[2];         // usable tokens of the K tile in each buffer
-    float fin[MAXS][3][32];    // final m_ref, m_true, l of every row
-};
-// after the last PV, the P^T buffers hold each O wave's 32 x D f16 tile of O (write_partial)
-static_assert(sizeof(FwdSmem<128>::p) >= MAXS * 32 * 128 * 2, "P buffers too small for the O tiles");
 
 // write a row tile's partials: per row the max in natural-log units, the sum of exp
 // relative to it, and the normalized output O = acc / l as f16 on a per-row scale (the
@@ -147,98 +126,6 @@ __device__ __forceinline__ void s_qk(const uint16_t *K, const bf16x8_t *qf, int 
     }
 }
 
-// S wave: online softmax of one tile's S^T, P^T (bf16) and the rescale factor to LDS.
-template <int D>
-__device__ __forceinline__ void s_softmax(f32x16_t *s, uint64_t okm, float &m_ref, float &m_true, float &l, int c32,
-                                          int hf, int lane, bool need_mask, int lim, float sl2, uint4 *pdst,
-                                          float *adst, int *rdst) {
-    // element i of s[t2] <-> token t2*32 + (i/4)*8 + hf*4 + i%4
-    if (need_mask) {
-        const uint64_t okh = okm >> (hf * 4);
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int tk = t2 * 32 + (i >> 2) * 8 + (i & 3);
-                const bool ok = ((okh >> tk) & 1) && tk < lim;
-                s[t2][i] = ok ? s[t2][i] : -INFINITY;
-            }
-    }
-    float mt = -INFINITY;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[t2][i]);
-    mt = ma_max_xor32(mt);
-    m_true = fmaxf(m_true, mt);
-    const bool need = (mt - m_ref) * sl2 > LAZY_LOG2;   // false for NaN (both -inf)
-    if (__any(need)) {
-        const float m_new = need ? mt : m_ref;
-        const float alpha = (m_new == m_ref) ? 1.0f : __builtin_amdgcn_exp2f((m_ref - m_new) * sl2);
-        l *= alpha;
-        m_ref = m_new;
-        if (hf == 0) adst[c32] = alpha;
-        if (lane == 0) *rdst = 1;
-    } else if (lane == 0) {
-        *rdst = 0;
-    }
-    const float off = (m_ref == -INFINITY) ? 0.f : -m_ref * sl2;
-    float ls = 0.f;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t2][i], sl2, off));
-            s[t2][i] = p;
-            ls += p;
-        }
-    l += ma_sum_xor32(ls);
-    // P^T chunk c = 16 tokens: the lane's s[c/2][8*(c%2) .. +7]
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        bf16x8_t pb;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pb[j] = (__bf16)s[c >> 1][(c & 1) * 8 + j];
-        pdst[c * 64 + lane] = __builtin_bit_cast(uint4, pb);
-    }
-}
-
-// O wave, one tile: O^T = alpha * O^T + V^T P^T.
-template <int D>
-__device__ __forceinline__ void o_tile(const uint16_t *Vt, const uint4 *psrc, const float *asrc, int resc,
-                                       f32x16_t *acc, int c32, int hf, int lane) {
-    constexpr int VS = TILE + 8;
-    constexpr int NDT = D / 32;
-    if (resc) {
-        const float a = asrc[c32];
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] *= a;
-    }
-    // chunk c+1's P^T and V^T fragments are loaded before chunk c's MFMAs; within a chunk
-    // the D/32 accumulators alternate, so no MFMA waits on the previous one
-    const uint16_t *vrow = &Vt[c32 * VS + hf * 8];
-    bf16x8_t pc = __builtin_bit_cast(bf16x8_t, psrc[lane]);
-    bf16x8_t va[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) va[dt] = *(const bf16x8_t *)&vrow[dt * 32 * VS];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        bf16x8_t nv[NDT], np = pc;
-        if (c + 1 < 4) {
-            np = __builtin_bit_cast(bf16x8_t, psrc[(c + 1) * 64 + lane]);
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) nv[dt] = *(const bf16x8_t *)&vrow[dt * 32 * VS + (c + 1) * 16];
-        }
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = ma_mfma32(va[dt], pc, acc[dt]);
-        if (c + 1 < 4) {
-            pc = np;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) va[dt] = nv[dt];
-        }
-    }
-}
-
 // Workgroup index -> (segment, lane bh, row group, split).  Prefix splits first, the
 // current-block workgroups last (they are short, so they fill in behind the splits).
 struct Work {
@@ -267,9 +154,166 @@ struct DSrc {
     const uint8_t *mask;  // liveness by absolute token index, or null
 };
 
-// The current block of one (lane, row group), for the packed kernel: a few 64-token tiles
-// staged synchronously from the 16-bit current K/V (no pipeline), then S^T, softmax
-// (block-causal mask) and PV as in the main loop; the partial goes to slot nsplit.
+// ---------------------------------------------------------------- pass 1
+// Every compute wave does S, softmax and PV of its own row tile (P never leaves its
+// registers); staging is spread over all 8 waves.  After the loop the K / V buffers hold
+// each wave's O tile for the partial write.
+constexpr int NTH = 512;
+constexpr int KLANES = NTH / 2;
+
+constexpr int NBUF = 3;   // K / V buffers: S of tile i+1 is issued while tile i is finished
+
+template <int D>
+struct FwdSmem {
+    union {
+        struct {
+            KTileL<D> kt[NBUF];
+            VTileL<D> vt[NBUF];
+        } t;
+        uint4 o[MAXS][4 * D];   // 32 x D f16 per row tile (write_partial)
+    } u;
+    uint64_t kmask[NBUF];
+};
+
+// s_softmax with the probabilities kept in registers: pb[c] = P^T chunk c (16 tokens) in
+// the register order of the PV B operand; returns whether the reference max was raised,
+// in which case the accumulator must first be scaled by alpha (the lane's row's factor).
+template <int D>
+__device__ __forceinline__ bool s_softmax_r(f32x16_t *s, uint64_t okm, float &m_ref, float &m_true, float &l,
+                                            int hf, bool need_mask, int lim, float sl2, bf16x8_t *pb,
+                                            float &alpha) {
+    if (need_mask) {
+        const uint64_t okh = okm >> (hf * 4);
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int tk = t2 * 32 + (i >> 2) * 8 + (i & 3);
+                const bool ok = ((okh >> tk) & 1) && tk < lim;
+                s[t2][i] = ok ? s[t2][i] : -INFINITY;
+            }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[t2][i]);
+    mt = ma_max_xor32(mt);
+    m_true = fmaxf(m_true, mt);
+    const bool need = (mt - m_ref) * sl2 > LAZY_LOG2;   // false for NaN (both -inf)
+    bool resc = false;
+    alpha = 1.0f;
+    if (__any(need)) {
+        const float m_new = need ? mt : m_ref;
+        alpha = (m_new == m_ref) ? 1.0f : __builtin_amdgcn_exp2f((m_ref - m_new) * sl2);
+        l *= alpha;
+        m_ref = m_new;
+        resc = true;
+    }
+    const float off = (m_ref == -INFINITY) ? 0.f : -m_ref * sl2;
+    float ls = 0.f;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t2][i], sl2, off));
+            s[t2][i] = p;
+            ls += p;
+        }
+    l += ma_sum_xor32(ls);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)s[c >> 1][(c & 1) * 8 + j];
+    return resc;
+}
+
+// The softmax of s_softmax_r in two parts, free of branches, so that the next tile's S^T
+// MFMAs can be interleaved with its exp2 part.  Part 1: the tile max, the lazily raised
+// reference max and the factor alpha (1 exactly where the reference stays, so l * alpha
+// and acc * alpha leave those rows' bits unchanged); returns whether this lane's row
+// raised it.
+__device__ __forceinline__ bool sm_max(const f32x16_t *s, float &m_ref, float &m_true, float &l, float sl2,
+                                       float &alpha, float &off) {
+    float mt = -INFINITY;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[t2][i]);
+    mt = ma_max_xor32(mt);
+    m_true = fmaxf(m_true, mt);
+    const bool need = (mt - m_ref) * sl2 > LAZY_LOG2;   // false for NaN (both -inf)
+    const float m_new = need ? mt : m_ref;
+    alpha = (m_new == m_ref) ? 1.0f : __builtin_amdgcn_exp2f((m_ref - m_new) * sl2);
+    l *= alpha;
+    m_ref = m_new;
+    off = (m_ref == -INFINITY) ? 0.f : -m_ref * sl2;
+    return need;
+}
+// S^T of the next tile (s_qk's MFMAs, in s_qk's order) interleaved in issue order with
+// the current tile's probabilities: after each MFMA the exp2 of the next few elements,
+// so that this wave's VALU work runs while its MFMAs are in the matrix pipe.  The same
+// arithmetic as s_qk followed by the exp2 part of s_softmax_r.
+template <int D>
+__device__ __forceinline__ void qk_exp(const uint16_t *K, const bf16x8_t *qf, int c32, int hf, f32x16_t *sn,
+                                       f32x16_t *sc, float &l, float sl2, float off, bf16x8_t *pb) {
+    constexpr int KS = D + 8;
+    constexpr int NKS = D / 16;
+    constexpr int EPM = 32 / (2 * NKS);   // probabilities per MFMA
+    sn[0] = f32x16_t{};
+    sn[1] = f32x16_t{};
+    const uint16_t *k0 = &K[c32 * KS + hf * 8];
+    const uint16_t *k1 = &K[(32 + c32) * KS + hf * 8];
+    bf16x8_t ka0 = *(const bf16x8_t *)k0, ka1 = *(const bf16x8_t *)k1;
+    float ls = 0.f;
+    auto expo = [&](int e0) {
+#pragma unroll
+        for (int e = e0; e < e0 + EPM; ++e) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e >> 4][e & 15], sl2, off));
+            sc[e >> 4][e & 15] = p;
+            ls += p;
+        }
+    };
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        bf16x8_t na0 = ka0, na1 = ka1;
+        if (ks + 1 < NKS) {
+            na0 = *(const bf16x8_t *)(k0 + (ks + 1) * 16);
+            na1 = *(const bf16x8_t *)(k1 + (ks + 1) * 16);
+        }
+        sn[0] = ma_mfma32(ka0, qf[ks], sn[0]);
+        expo((2 * ks) * EPM);
+        __builtin_amdgcn_sched_barrier(0);
+        sn[1] = ma_mfma32(ka1, qf[ks], sn[1]);
+        expo((2 * ks + 1) * EPM);
+        __builtin_amdgcn_sched_barrier(0);
+        ka0 = na0;
+        ka1 = na1;
+    }
+    l += ma_sum_xor32(ls);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pb[c][j] = (__bf16)sc[c >> 1][(c & 1) * 8 + j];
+}
+
+// O^T += V^T P^T for one tile, P^T from registers: chunk by chunk (16 tokens), the D/32
+// accumulators alternating
+template <int D>
+__device__ __forceinline__ void pv_regs(const uint16_t *Vt, const bf16x8_t *pb, f32x16_t *acc, int c32, int hf) {
+    constexpr int VS = TILE + 8;
+    constexpr int NDT = D / 32;
+    const uint16_t *vrow = &Vt[c32 * VS + hf * 8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+            acc[dt] = ma_mfma32(*(const bf16x8_t *)&vrow[dt * 32 * VS + c * 16], pb[c], acc[dt]);
+}
+
+// The current block of one (lane, row group) for the packed kernel: its tiles staged
+// synchronously by every thread from the 16-bit current K/V, then S^T, softmax
+// (block-causal mask) and PV; the partial goes to slot nsplit.
 template <int D>
 __device__ __forceinline__ void cur_segment(const FwdArgs &a, const Work &wk, FwdSmem<D> &S) {
     constexpr int NKS = D / 16;
@@ -283,82 +327,64 @@ __device__ __forceinline__ void cur_segment(const FwdArgs &a, const Work &wk, Fw
     const int nt = (Tc + TILE - 1) / TILE;
     const int nS = min(MAXS, a.row_tiles - wk.rg * MAXS);
     const bool is_s = wave < nS;
-    const bool is_o = wave >= 8 && wave - 8 < nS;
-    const int rw = is_o ? wave - 8 : wave;
-    const int row = (wk.rg * MAXS + rw) * 32 + c32;
+    const int rtile = wk.rg * MAXS + wave;
+    const int row = rtile * 32 + c32;
     const bool row_ok = row < a.R;
     const int qpos = a.q_pos0 + (row_ok ? row % a.T : 0);
     const bool causal = a.causal > 0;
-    // S waves and the other waves run separate loops with the same barriers (as in the
-    // main path), so Q fragments and accumulators never share registers
-    if (wave < 7) {
-        bf16x8_t qf[NKS];
-        if (is_s) {
-            const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
-            const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
+    bf16x8_t qf[NKS];
+    if (is_s) {
+        const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
+        const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
-        }
-        float m_ref = -INFINITY, m_true = -INFINITY, l = 0.f;
-        for (int i = 0; i < nt; ++i) {
-            const int n0 = i * TILE;
-            __syncthreads();  // tile staged
-            if (is_s) {
-                f32x16_t sv[2];
-                s_qk<D>(S.kt[0].k, qf, c32, hf, sv);
-                const uint64_t okm = S.kmask[0];
-                const int lim = causal ? (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4 : TILE;
-                s_softmax<D>(sv, okm, m_ref, m_true, l, c32, hf, lane, true, lim, a.sl2, &S.p[0][rw][0][0],
-                             S.alpha[0][rw], &S.resc[0][rw]);
-            }
-            __syncthreads();  // P ready
-            __syncthreads();  // PV done, buffers free
-        }
-        if (is_s && hf == 0) {
-            S.fin[rw][0][c32] = m_ref;
-            S.fin[rw][1][c32] = m_true;
-            S.fin[rw][2][c32] = l;
-        }
-        __syncthreads();
-    } else {
-        f32x16_t acc[NDT];
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-        const int sl = tid - 7 * 64, nsl = NTH - 7 * 64;   // staging lanes
-        for (int i = 0; i < nt; ++i) {
-            const int n0 = i * TILE;
-            const int valid = Tc - n0;
-            uint32_t w[8];
-            const char *kb = kc.base + (int64_t)n0 * kc.sn * kc.esz;
-            for (int u = sl; u < TILE * D / 8; u += nsl) {
-                const bool ok = load_k_dense<D>(w, kb, kc.sn, kc.dtype, kc.esz, u, valid);
-                store_k_dense<D>(S.kt[0].k, w, u, kc.dtype, ok);
-            }
-            const char *vb = vc.base + (int64_t)n0 * vc.sn * vc.esz;
-            for (int u = sl; u < TILE / 2 * D / 8; u += nsl) {
-                const int tp = u % (TILE / 2);
-                load_v_dense<D>(w, vb, vc.sn, vc.dtype, vc.esz, u, valid);
-                store_v_dense<D>(S.vt[0].vt, w, u, vc.dtype, 2 * tp < valid, 2 * tp + 1 < valid);
-            }
-            if (wave == 7) {
-                const uint64_t m = __ballot(lane < valid);
-                if (lane == 0) S.kmask[0] = m;
-            }
-            __syncthreads();  // tile staged
-            __syncthreads();  // P ready
-            if (is_o) o_tile<D>(S.vt[0].vt, &S.p[0][rw][0][0], S.alpha[0][rw], S.resc[0][rw], acc, c32, hf, lane);
-            __syncthreads();  // PV done
-        }
-        __syncthreads();  // final statistics
-        if (is_o)
-            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, a.nsplit,
-                             wk.rg * MAXS + rw, c32, hf, lane, &S.p[0][0][0][0] + rw * (4 * D));
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
     }
+    float m_ref = -INFINITY, m_true = -INFINITY, l = 0.f;
+    f32x16_t acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
+    for (int i = 0; i < nt; ++i) {
+        const int n0 = i * TILE;
+        const int valid = Tc - n0;
+        uint32_t w[8];
+        const char *kb = kc.base + (int64_t)n0 * kc.sn * kc.esz;
+        for (int u = tid; u < TILE * D / 8; u += NTH) {
+            const bool ok = load_k_dense<D>(w, kb, kc.sn, kc.dtype, kc.esz, u, valid);
+            store_k_dense<D>(S.u.t.kt[0].k, w, u, kc.dtype, ok);
+        }
+        const char *vb = vc.base + (int64_t)n0 * vc.sn * vc.esz;
+        for (int u = tid; u < TILE / 2 * D / 8; u += NTH) {
+            const int tp = u % (TILE / 2);
+            load_v_dense<D>(w, vb, vc.sn, vc.dtype, vc.esz, u, valid);
+            store_v_dense<D>(S.u.t.vt[0].vt, w, u, vc.dtype, 2 * tp < valid, 2 * tp + 1 < valid);
+        }
+        if (wave == 0) {
+            const uint64_t m = __ballot(lane < valid);
+            if (lane == 0) S.kmask[0] = m;
+        }
+        __syncthreads();  // tile staged
+        if (is_s) {
+            f32x16_t sv[2];
+            s_qk<D>(S.u.t.kt[0].k, qf, c32, hf, sv);
+            const int lim = causal ? (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4 : TILE;
+            bf16x8_t pb[4];
+            float alpha;
+            if (s_softmax_r<D>(sv, S.kmask[0], m_ref, m_true, l, hf, true, lim, a.sl2, pb, alpha)) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+            }
+            pv_regs<D>(S.u.t.vt[0].vt, pb, acc, c32, hf);
+        }
+        __syncthreads();  // buffers free
+    }
+    if (is_s) write_partial<D>(a, acc, m_ref, m_true, l, bh, a.nsplit, rtile, c32, hf, lane, &S.u.o[wave][0]);
 }
 
-template <int D, int SRC>
+// FULL (packed only): no slot mask and every split a run of whole 64-token tiles (the host
+// checks nq % 64 == 0), so only the whole-tile staging path is built
+template <int D, int SRC, bool FULL>
 __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     __shared__ FwdSmem<D> S;
     using Shape = StageShape<KLANES, D, SRC == 0 ? ST_PACKED : ST_DENSE>;
@@ -377,7 +403,6 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     const int wave = tid >> 6, lane = tid & 63, c32 = lane & 31, hf = lane >> 5;
 
     const Lane L = make_lane(a.pre, b, h, bh);
-    // token range of this workgroup
     int n_beg, n_end;
     if (wk.cur) {
         n_beg = 0;
@@ -400,23 +425,13 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         }
     }
 
-    // roles
     const int nS = min(MAXS, a.row_tiles - wk.rg * MAXS);
     const bool is_s = wave < nS;
-    const bool is_o = wave >= 8 && wave - 8 < nS;
-    const int rw = is_o ? wave - 8 : wave;          // row tile within the group
-    const int rtile = wk.rg * MAXS + rw;
+    const int rtile = wk.rg * MAXS + wave;
     const int row = rtile * 32 + c32;
     const bool row_ok = row < a.R;
-    // staging lanes: waves 7..15 (the O waves and two staging-only waves); the S waves keep
-    // their registers for two tiles of S^T and the Q fragments
-    const int st_lane = wave >= 7 ? tid - 7 * 64 : -1;
-    const bool is_k = st_lane >= 0 && st_lane < KLANES;
-    // packed: the V lanes of wave 11 (SIMD 3) stage here; those of waves 12..14 are taken
-    // by wave 15 (also SIMD 3, three items per lane), so the three SIMDs that carry two S
-    // and two O waves do no V staging (a SIMD's full-rate VALU and MFMA time add up)
-    const bool is_v = st_lane >= KLANES && st_lane < (SRC == 0 ? KLANES + 64 : NSTAGE);
-    const int kl = st_lane, vl = st_lane - KLANES;
+    const bool is_k = tid < KLANES;
+    const int kl = tid, vl = tid - KLANES;
 
     auto tile_n0 = [&](int i) { return n_beg + i * TILE; };
     auto live = [&](int j) {
@@ -431,19 +446,16 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
 
     StageRegs<Shape::NW> pr;
     pr.flags = 0;
-    // K lanes: global loads of tile i into pr (or another register set); the dequant /
-    // copy into a K buffer
-    // packed whole tiles: this lane's item offsets, once
     uint2 item_off = uint2{0u, 0u};
     if constexpr (SRC == 0) {
         if (is_k && kl < Shape::NK) item_off = k_item_offsets<D>(L, kl);
-        else if (is_v && vl < Shape::NV) item_off = v_item_offsets<D>(L, vl);
+        else if (!is_k && vl < Shape::NV) item_off = v_item_offsets<D>(L, vl);
     }
-    const bool fast_tiles = SRC == 0 && !L.mask;   // whole tiles of an unmasked packed prefix
-    auto load_k_into = [&](StageRegs<Shape::NW> &pr, int i) {
+    const bool fast_tiles = SRC == 0 && (FULL || !L.mask);
+    auto load_k = [&](int i) {
         const int n0 = tile_n0(i);
         if constexpr (SRC == 0) {
-            if (fast_tiles && n0 + TILE <= n_end) {
+            if (FULL || (fast_tiles && n0 + TILE <= n_end)) {
                 pr.flags = kl < TILE ? 256u : 0u;
                 if (kl < Shape::NK) {
                     const int64_t g0 = n0 / KGRP;
@@ -455,19 +467,20 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         }
         pr.flags = (kl < TILE && live(n0 + kl)) ? 256u : 0u;
         if constexpr (SRC == 0) {
-            if (kl < Shape::NK) load_k_packed<D>(pr.w, L, kl, n0, n_end);
+            if constexpr (!FULL) {
+                if (kl < Shape::NK) load_k_packed<D>(pr.w, L, kl, n0, n_end);
+            }
         } else {
             const char *base = ds.k + (int64_t)(n0 - ds.tok0) * ds.sk * ds.esz;
 #pragma unroll
             for (int r = 0; r < Shape::KPL; ++r) {
                 const int u = kl + r * KLANES;
                 if (u < Shape::NK && load_k_dense<D>(&pr.w[4 * r], base, ds.sk, ds.dtype, ds.esz, u, n_end - n0))
-                    pr.flags |= 1u << r;   // bit r: item r's token below the end
+                    pr.flags |= 1u << r;
             }
         }
     };
-    auto load_k = [&](int i) { load_k_into(pr, i); };
-    auto store_k_from = [&](StageRegs<Shape::NW> &pr, uint16_t *Ks, uint64_t &km) {
+    auto store_k = [&](uint16_t *Ks, uint64_t &km) {
         if constexpr (SRC == 0) {
             if (kl < Shape::NK) store_k_packed<D>(Ks, pr.w, kl);
         } else {
@@ -482,29 +495,23 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             if (kl == 0) km = m;
         }
     };
-    auto store_k = [&](uint16_t *Ks, uint64_t &km) { store_k_from(pr, Ks, km); };
-    // V lanes: global loads of tile i into pr (or another register set); the dequant /
-    // copy into a V buffer
-    // packed V item vx (offsets ox from the tile start) of tile i into pr
-    auto load_vp_item = [&](StageRegs<Shape::NW> &pr, int i, int vx, uint2 ox) {
-        const int n0 = tile_n0(i);
-        if (fast_tiles && n0 + TILE <= n_end) {
-            if (vx < Shape::NV) {
-                load_v_packed_fast(pr.w, L.vq + (int64_t)n0 * L.vq_n, L.vs + (int64_t)n0 * L.vs_n,
-                                   L.vz + (int64_t)n0 * L.vs_n, L.vq_n, L.vs_n, ox);
-                pr.flags = 3u;
-            }
-            return;
-        }
-        if (vx < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vx, n0, n_end);
-    };
-    auto load_v_into = [&](StageRegs<Shape::NW> &pr, int i) {
+    auto load_v = [&](int i) {
         const int n0 = tile_n0(i);
         if constexpr (SRC == 0) {
-            load_vp_item(pr, i, vl, item_off);
+            if (FULL || (fast_tiles && n0 + TILE <= n_end)) {
+                if (vl < Shape::NV) {
+                    load_v_packed_fast(pr.w, L.vq + (int64_t)n0 * L.vq_n, L.vs + (int64_t)n0 * L.vs_n,
+                                       L.vz + (int64_t)n0 * L.vs_n, L.vq_n, L.vs_n, item_off);
+                    pr.flags = 3u;
+                }
+                return;
+            }
+            if constexpr (!FULL) {
+                if (vl < Shape::NV) load_v_packed<D>(pr.w, pr.flags, L, vl, n0, n_end);
+            }
         } else {
             const char *base = ds.v + (int64_t)(n0 - ds.tok0) * ds.sv * ds.esz;
-            pr.flags = 0u;   // bits 2r, 2r+1: item r's two tokens live
+            pr.flags = 0u;
 #pragma unroll
             for (int r = 0; r < Shape::VPL; ++r) {
                 const int u = vl + r * KLANES;
@@ -517,8 +524,7 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         }
     };
-    auto load_v = [&](int i) { load_v_into(pr, i); };
-    auto store_v_from = [&](StageRegs<Shape::NW> &pr, uint16_t *Vt) {
+    auto store_v = [&](uint16_t *Vt) {
         if constexpr (SRC == 0) {
             if (vl < Shape::NV) store_v_packed<D>(Vt, pr.w, vl);
         } else {
@@ -531,141 +537,110 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         }
     };
-    auto store_v = [&](uint16_t *Vt) { store_v_from(pr, Vt); };
+    auto load_tile = [&](int i) {
+        if (is_k) load_k(i);
+        else load_v(i);
+    };
+    // the buffer's byte offset is made opaque to the compiler, so that the row addresses of
+    // a store are immediate offsets from one register instead of per-buffer constants held
+    // across the loop (the third buffer lies beyond the 16-bit immediate range)
+    auto store_tile = [&](int buf) {
+        if (is_k) {
+            int off = buf * (int)sizeof(KTileL<D>);
+            asm volatile("" : "+v"(off));
+            store_k((uint16_t *)((char *)S.u.t.kt[0].k + off), S.kmask[buf]);
+        } else {
+            int off = buf * (int)sizeof(VTileL<D>);
+            asm volatile("" : "+v"(off));
+            store_v((uint16_t *)((char *)S.u.t.vt[0].vt + off));
+        }
+    };
 
     const int qpos = a.q_pos0 + (row_ok ? row % a.T : 0);
     const bool causal = wk.cur && a.causal > 0;
 
-    // The two branches run separate loops (wave-uniform) with the same barrier count, so
-    // the S state (Q fragments, staging registers) and the O state (accumulators, PV
-    // operands) never share registers.
-    if (wave < 7) {
-        // ---- S waves
-        bf16x8_t qf[NKS];
-        float m_ref = -INFINITY, m_true = -INFINITY, l = 0.f;
+    // prologue: tiles 0 and 1 staged, tile 2's loads in flight; Q of the row tile
+    if (nt > 0) load_tile(0);
+    bf16x8_t qf[NKS];
+    if (is_s) {
+        const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
+        const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
+    }
+    if (nt > 0) store_tile(0);
+    if (nt > 1) {
+        load_tile(1);
+        store_tile(1);
+    }
+    if (nt > 2) load_tile(2);
+    __syncthreads();
+
+    float m_ref = -INFINITY, m_true = -INFINITY, l = 0.f;
+    f32x16_t acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
+    // Iteration it: S^T of tile it+1 is issued first (its MFMAs run while this wave does the
+    // softmax of tile it, whose S^T the previous iteration issued), then PV of tile it, then
+    // tile it+2 is staged into the buffer tiles it-1 used (both read before the last two
+    // barriers) and the loads of tile it+3 are issued.
+    f32x16_t sa[2], sb[2];
+    if (is_s && nt > 0) s_qk<D>(S.u.t.kt[0].k, qf, c32, hf, sa);
+    auto step = [&](int it, f32x16_t *sc, f32x16_t *sn) {
+        const int cb = it % NBUF;
+        const uint64_t mc = S.kmask[cb];
         if (is_s) {
-            const int g = row_ok ? row / a.T : 0, t = row_ok ? row % a.T : 0;
-            const int64_t qb = b * a.q.s[0] + (int64_t)(h * a.G + g) * a.q.s[1] + (int64_t)t * a.q.s[2];
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = ma_load8_as_bf16(a.q.ptr, qb + ks * 16 + hf * 8, a.q.dtype);
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = row_ok ? qf[ks] : bf16x8_t{};
-        }
-        __syncthreads();  // prologue staging done
-        // Iteration it: the S waves do the softmax of tile it and then issue S^T of tile it+1
-        // (K is staged two tiles ahead).  Tile masks travel with S^T.
-        f32x16_t sa[2], sb[2];
-        uint64_t ma = 0, mb = 0;
-        if (is_s && nt > 0) {
-            s_qk<D>(S.kt[0].k, qf, c32, hf, sa);
-            ma = S.kmask[0];
-        }
-        __syncthreads();  // K buffer 0 is read: the first iteration stages tile 2 into it
-        // The softmax of tile it (VALU) comes first and S^T of tile it+1 (MFMA) second: the
-        // O waves start a tile with their PV MFMAs and then stage (VALU), so the two kinds
-        // of waves keep the matrix pipe and the VALU busy at the same time.
-        auto step = [&](int it, f32x16_t *sc, uint64_t mc, f32x16_t *sn, uint64_t &mn) {
-            const int cb = it & 1;
-            if (is_s && it < nt) {
+            if constexpr (!FULL) {
                 const int n0 = tile_n0(it);
                 const int lim = causal ? (qpos / a.causal + 1) * a.causal - a.c_pos0 - n0 - hf * 4 : TILE;
-                const bool need_mask = causal || mc != ~0ull;
-                s_softmax<D>(sc, mc, m_ref, m_true, l, c32, hf, lane, need_mask, lim, a.sl2, &S.p[cb][rw][0][0],
-                             S.alpha[cb][rw], &S.resc[cb][rw]);
-            }
-            if (is_s && it + 1 < nt) {
-                s_qk<D>(S.kt[cb ^ 1].k, qf, c32, hf, sn);
-                mn = S.kmask[cb ^ 1];
-            }
-            __syncthreads();
-        };
-        int it = 0;
-        for (; it + 1 <= nt; it += 2) {
-            step(it, sa, ma, sb, mb);
-            step(it + 1, sb, mb, sa, ma);
-        }
-        if (it <= nt) step(it, sa, ma, sb, mb);
-        if (is_s && hf == 0) {
-            S.fin[rw][0][c32] = m_ref;
-            S.fin[rw][1][c32] = m_true;
-            S.fin[rw][2][c32] = l;
-        }
-        __syncthreads();
-    } else if (SRC == 0 && wave == NTH / 64 - 1) {
-        // ---- packed V staging of V lanes 64 .. 255 (three items per lane): tile it in
-        // iteration it, the loads of tile it+1 behind it; the same barriers as the O waves
-        constexpr int NX = 3;
-        StageRegs<Shape::NW> vr[NX];
-        uint2 vo[NX];
-        int vx[NX];
+                if (causal || mc != ~0ull) {
+                    const uint64_t okh = mc >> (hf * 4);
 #pragma unroll
-        for (int j = 0; j < NX; ++j) {
-            vx[j] = 64 * (j + 1) + lane;
-            vr[j].flags = 0;
-            vo[j] = vx[j] < Shape::NV ? v_item_offsets<D>(L, vx[j]) : uint2{0u, 0u};
-        }
-        if (nt > 0) {
+                    for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-            for (int j = 0; j < NX; ++j) load_vp_item(vr[j], 0, vx[j], vo[j]);
-        }
-        __syncthreads();
-        __syncthreads();
-        for (int it = 0; it <= nt; ++it) {
-            if (it < nt) {
-                uint16_t *Vt = S.vt[it & 1].vt;
-#pragma unroll
-                for (int j = 0; j < NX; ++j)
-                    if (vx[j] < Shape::NV) store_v_packed<D>(Vt, vr[j].w, vx[j]);
-                if (it + 1 < nt) {
-#pragma unroll
-                    for (int j = 0; j < NX; ++j) load_vp_item(vr[j], it + 1, vx[j], vo[j]);
+                        for (int i = 0; i < 16; ++i) {
+                            const int tk = t2 * 32 + (i >> 2) * 8 + (i & 3);
+                            const bool ok = ((okh >> tk) & 1) && tk < lim;
+                            sc[t2][i] = ok ? sc[t2][i] : -INFINITY;
+                        }
                 }
             }
-            __syncthreads();
-        }
-        __syncthreads();  // final statistics of the S waves
-    } else {
-        // ---- O waves (PV one tile behind the S waves) and staging: K lanes stage tile it+2,
-        // V lanes tile it
-        f32x16_t acc[NDT];
+            float alpha, off;
+            const bool resc = __any(sm_max(sc, m_ref, m_true, l, a.sl2, alpha, off));
+            // S^T of tile it+1 (issued on the last tile too: that buffer holds an earlier
+            // tile, whose result is never used), its 16 MFMAs interleaved with the exp2 part
+            bf16x8_t pb[4];
+            qk_exp<D>(S.u.t.kt[(it + 1) % NBUF].k, qf, c32, hf, sn, sc, l, a.sl2, off, pb);
+            if (resc) {
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16_t{};
-        // prologue: the loads of K tiles 0 and 1 issued together (two register sets) and V
-        // tile 0 in flight; K tile 0 staged before the first barrier, K tile 1 (buffer 1)
-        // while the S waves compute S^T of tile 0 from buffer 0, then K tile 2 in flight
-        StageRegs<Shape::NW> pr1;
-        pr1.flags = 0;
-        if (is_k) {
-            if (nt > 0) load_k(0);
-            if (nt > 1) load_k_into(pr1, 1);
-            if (nt > 0) store_k(S.kt[0].k, S.kmask[0]);
-        } else if (is_v && nt > 0) {
-            load_v(0);
-        }
-        __syncthreads();
-        if (is_k) {
-            if (nt > 1) store_k_from(pr1, S.kt[1].k, S.kmask[1]);
-            if (nt > 2) load_k(2);
-        }
-        __syncthreads();  // the S waves have read K tile 0 out of buffer 0; K tile 1 is staged
-        for (int it = 0; it <= nt; ++it) {
-            const int cb = it & 1, pb = cb ^ 1;
-            if (is_o && it >= 1)
-                o_tile<D>(S.vt[pb].vt, &S.p[pb][rw][0][0], S.alpha[pb][rw], S.resc[pb][rw], acc, c32, hf, lane);
-            if (is_k && it + 2 < nt) {
-                store_k(S.kt[cb].k, S.kmask[cb]);
-                if (it + 3 < nt) load_k(it + 3);
-            } else if (is_v && it < nt) {
-                store_v(S.vt[cb].vt);
-                if (it + 1 < nt) load_v(it + 1);
+                for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
             }
-            __syncthreads();
+#ifndef X_NOPV
+            pv_regs<D>(S.u.t.vt[cb].vt, pb, acc, c32, hf);
+#else
+            acc[0][0] += (float)pb[0][0] + (float)pb[1][1] + (float)pb[2][2] + (float)pb[3][3];
+#endif
         }
-        __syncthreads();  // final statistics of the S waves
-        if (is_o)
-            write_partial<D>(a, acc, S.fin[rw][0][c32], S.fin[rw][1][c32], S.fin[rw][2][c32], bh, slot, rtile, c32,
-                             hf, lane, &S.p[0][0][0][0] + rw * (4 * D));
+#ifndef X_NOSTAGE
+        if (it + 2 < nt) {
+            store_tile((it + 2) % NBUF);
+#ifndef X_NOLOAD
+            if (it + 3 < nt) load_tile(it + 3);
+#endif
+        }
+#endif
+        __syncthreads();
+    };
+    int it = 0;
+    for (; it + 2 <= nt; it += 2) {
+        step(it, sa, sb);
+        step(it + 1, sb, sa);
     }
+    if (it < nt) step(it, sa, sb);
+    // every wave is past its last read of the K / V buffers: they take the O tiles
+    if (is_s) write_partial<D>(a, acc, m_ref, m_true, l, bh, slot, rtile, c32, hf, lane, &S.u.o[wave][0]);
 }
 
 // Pass 2: grid (R, B*H), 128 threads = 8 split lanes x 16 channel octets.  Split lane
@@ -777,7 +752,8 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
     }
 }
 
-// Tokens per split: about one workgroup per CU (one 133 KB-LDS workgroup fits a CU), with
+// Tokens per split: about one workgroup per CU (a workgroup's 256 VGPRs per lane and
+// 108 KB of LDS fill a CU), with
 // one CU per (lane, row group) left for the current block's workgroups, so every
 // workgroup of the launch runs in the first dispatch wave; at least one 64-token tile.
 // Short prefixes (a sub-step's 2 048 selected entries) thus spread over many CUs: each
@@ -919,7 +895,14 @@ int launch_partial_d(const Plan &pl, hipStream_t st) {
         fa.tok_beg = 0;
         fa.tok_end = nq;
         fa.with_cur = cur_in_packed;
-        hipLaunchKernelGGL((splitk_fwd_kernel<D, 0>), dim3((nsq + fa.with_cur) * units), dim3(NTH), 0, st, fa);
+        // whole tiles everywhere: no slot mask, a packed part of whole tiles (every split is)
+        const bool full = !fa.pre.mask && nq % TILE == 0;
+        if (full)
+            hipLaunchKernelGGL((splitk_fwd_kernel<D, 0, true>), dim3((nsq + fa.with_cur) * units), dim3(NTH), 0, st,
+                               fa);
+        else
+            hipLaunchKernelGGL((splitk_fwd_kernel<D, 0, false>), dim3((nsq + fa.with_cur) * units), dim3(NTH), 0,
+                               st, fa);
     }
     if (!cur_in_packed) {
         fa.nsp = nsf;
@@ -927,7 +910,7 @@ int launch_partial_d(const Plan &pl, hipStream_t st) {
         fa.tok_beg = nq;
         fa.tok_end = nq + nf;
         fa.with_cur = 1;
-        hipLaunchKernelGGL((splitk_fwd_kernel<D, 1>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
+        hipLaunchKernelGGL((splitk_fwd_kernel<D, 1, false>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
     }
     return ma_check_launch("ma_splitk_partial");
 }
