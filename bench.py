@@ -99,7 +99,9 @@ def time_graph(fn, steps, warmup, inner=1):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # captured on the warm-up stream, so that what fn() keeps per stream (the select
+    # state) already exists: nothing is allocated or zero-filled during capture
+    with torch.cuda.graph(g, stream=side):
         for _ in range(inner):
             fn()
     for _ in range(warmup):
@@ -170,8 +172,8 @@ def main():
         bench_substep(a)
         return
     from maskahead_amd import _native as N
-    from maskahead_amd.kernels import (gather_packed_kv, prefix_scores, prefix_scores_topk,
-                                       quantize_key_groups_into, quantize_values_into, splitk_attention)
+    from maskahead_amd.kernels import (Step0Buffers, prefix_scores, quantize_key_groups_into, quantize_values_into,
+                                       splitk_attention, step0_select)
     from maskahead_amd.kernels.splitk import Prefix
     from maskahead_amd.workloads import CONFIGS, layer_inputs, packed_layout
 
@@ -191,20 +193,6 @@ def main():
     kdev, vdev = k.to(dev), v.to(dev)
     rows = list(range(sh.t))          # the whole block in order (mode "all"), as the session passes it
 
-    class View:
-        """the packed cache of one layer, as the gather reads it (cache.py:LayerView)"""
-        k_bits = v_bits = 4
-        length = quantized_length = sh.n
-        residual_length = 0
-        key_token_group = value_channel_group = 32
-        k_fp = v_fp = k_residual = v_residual = None
-        head_dim = sh.d
-        key_mode = "channel"
-
-        def __init__(self, lay):
-            self.k_q, self.k_scale, self.k_zero = lay["kq"], lay["ks"], lay["kz"]
-            self.v_q, self.v_scale, self.v_zero = lay["vq"], lay["vs"], lay["vz"]
-
     layers = []
     for li in range(a.layers):
         lay = packed_layout(sh.b, sh.hkv, sh.n, sh.d, device=dev)
@@ -216,16 +204,20 @@ def main():
         prefix = Prefix(kq=lay["kq"], ks=lay["ks"], kz=lay["kz"], vq=lay["vq"], vs=lay["vs"], vz=lay["vz"],
                         nq=sh.n, kb=4, vb=4)
         compact_k = torch.empty((sh.b, sh.hkv, sh.read_k + sh.t, sh.d), dtype=torch.bfloat16, device=dev)
-        layers.append(dict(prefix=prefix, lay=lay, view=View(lay), ck=compact_k, cv=torch.empty_like(compact_k)))
+        layers.append(dict(prefix=prefix, lay=lay, ck=compact_k, cv=torch.empty_like(compact_k), bufs=Step0Buffers()))
     del kdev, vdev
     prefix, lay = layers[0]["prefix"], layers[0]["lay"]
     result = {}
 
+    step_ws = Step0Buffers()                 # one scratch workspace, shared by the layers
+
     def layer_step(L):
-        out, stats = splitk_attention(qg, L["prefix"], kcg, vcg, want_prefix=True, split_tokens=a.split_tokens)
-        # the score pass also builds the select's first histogram level (one launch less)
-        mass, score, idx = prefix_scores_topk(qg, L["prefix"], stats, rows, sh.read_k, value=True, rank="score")
-        gather_packed_kv(L["view"], idx, out_key=L["ck"][:, :, :sh.read_k], out_value=L["cv"][:, :, :sh.read_k])
+        # the session's step 0 (FastLayerPath.step0): one library call into the layer's own
+        # reused buffers -- split-K attention, value-aware scores building the select's first
+        # histogram level, the read-set top-k and the gather
+        out, _, mass, score, idx = step0_select(L["bufs"], qg, L["prefix"], kcg, vcg, rows, sh.read_k, value=True,
+                                                out_key=L["ck"][:, :, :sh.read_k],
+                                                out_value=L["cv"][:, :, :sh.read_k], workspace=step_ws)
         result["out"], result["idx"] = out, idx
 
     def step():

@@ -153,9 +153,9 @@ int ma_prefix_scores(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix 
  * GQA-reduced VALU pass for at most 16 rows (G*T2 <= 16) -- waves stream 32-token units
  * with no workgroup barrier, q . k by v_dot2c_f32_bf16 for every selection row, the value
  * centre from those rows of O_p only -- instead of 32-row MFMA tiles that are mostly
- * padding.  mode 0 (default) takes it for at most 8 rows (G 7 x T2 1, G 4 x T2 1-2) and
- * the MFMA pass otherwise, 1 forces the MFMA pass, 2 the VALU pass (calls above 16 rows
- * then fail); process-wide, for measurement and tests.  Returns the previous mode, or -1
+ * padding.  mode 0 (default) takes the MFMA pass for every row count (it measured as fast
+ * or faster at config 2's prefix), 1 forces the MFMA pass, 2 the VALU pass (calls above 16
+ * rows then fail); process-wide, for measurement and tests.  Returns the previous mode, or -1
  * for a bad mode.  No counterpart in the reference (Triton picks no variant). */
 int ma_prefix_scores_path(int mode);
 
@@ -194,6 +194,23 @@ int ma_topk_select_hist_ready(const float *rank, int64_t rank_stride, const uint
                               int64_t mask_stride, int rows, int n, int k, int64_t *idx, int64_t idx_stride,
                               float *values, void *state, int64_t state_bytes, void *workspace,
                               int64_t workspace_bytes, void *stream);
+
+/* Step 0 of a sparse layer in one call (the reference session's _fast_step0,
+ * session.py:1403-1454, which runs splitk_attention(want_prefix=True), prefix_scores,
+ * topk + sort and gather_packed_kv as four Python-level ops): enqueues, on `stream`,
+ * ma_splitk_attention (outputs out, mp, lp, op; split_tokens auto, no causal mask),
+ * ma_prefix_scores_hist (mass, and score when value = 1) with the read-set top-k's first
+ * level of rank 1 (mass) or 2 (score, value = 1), ma_topk_select_hist_ready (k ascending
+ * indices per (b, KV head) into idx [B, H, k] contiguous, dead slots of p->mask never
+ * selected) and, when k_out / v_out are given, ma_gather_kv of those entries -- the
+ * results of calling them one by one.  topk_state: as for ma_prefix_scores_hist (zero
+ * before, left zero).  workspace: ma_step0_workspace_bytes() bytes, 256-byte aligned. */
+int64_t ma_step0_workspace_bytes(int B, int H, int Hq, int T, int D, int nq, int nf);
+int ma_step0(ma_tensor4 q, int B, int Hq, int T, int D, const ma_prefix *p, int H, ma_tensor4 kc,
+             ma_tensor4 vc, int Tc, float scale, ma_tensor4 out, float *mp, float *lp, void *op,
+             const int32_t *q_rows, int T2, int value, int rank, int v_round, float *mass, float *score, int k,
+             int64_t *idx, ma_tensor4 k_out, ma_tensor4 v_out, void *topk_state, int64_t state_bytes,
+             void *workspace, int64_t workspace_bytes, void *stream);
 
 /* keep set of an eviction step (EvictionState.survivors, eviction.py:325-409, for the
  * score-ranked policies; capacity C = EvictionConfig.capacity, eviction.py:200-202): per

@@ -74,6 +74,9 @@ SIGNATURES = {
     "ma_prefix_scores_path": (_I, [_I]),
     "ma_prefix_scores_hist": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _P, _I, _P, _P, _P, _I, _F, _I, _I, _P,
                                    _P, _I, _P, _I64, _P]),
+    "ma_step0_workspace_bytes": (_I64, [_I, _I, _I, _I, _I, _I, _I]),
+    "ma_step0": (_I, [_T4, _I, _I, _I, _I, _PREF, _I, _T4, _T4, _I, _F, _T4, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P,
+                      _I, _P, _T4, _T4, _P, _I64, _P, _I64, _P]),
     "ma_keep_select": (_I, [_P, _I, _I64, _P, _I64, _I, _I, _I, _I, _I64, _P, _I64, _I64, _I, _P, _I64, _P,
                             _P, _I64, _P, _I64, _P]),
     "ma_value_score_workspace_bytes": (_I64, [_I, _I, _I]),

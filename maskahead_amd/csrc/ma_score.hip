@@ -783,7 +783,9 @@ __global__ void __launch_bounds__(NT) score_kernel(ScoreArgs a) {
 //     LDS, adds the other half's sum (lane ^ 32) and sums exp2(s * scale*log2e - c_r);
 //   * the next unit's loads are issued before the scores of this one.
 constexpr int SMALL_ROWS = 16;
-constexpr int AUTO_SMALL_ROWS = 8;           // the largest row count mode 0 sends here
+// the largest row count mode 0 sends here: none -- at config 2's prefix the padded MFMA
+// pass measured as fast or faster (7 rows: 16.8 vs 17.4 us; 14 rows: 16.8 vs 21.9 us)
+constexpr int AUTO_SMALL_ROWS = 0;
 constexpr int SM_NT = 256;                   // threads per workgroup
 constexpr int SM_WAVES = SM_NT / 64;
 constexpr int UNIT = KGRP;                   // tokens per unit
@@ -1065,8 +1067,8 @@ __global__ void __launch_bounds__(SNT) centre_kernel(const void *op, int op_dtyp
 
 int ma_validate_prefix(const ma_prefix *p, int D, const char *who);
 
-// 0: the VALU pass for at most AUTO_SMALL_ROWS selection rows, MFMA otherwise; 1: always
-// MFMA; 2: always VALU (calls with more than SMALL_ROWS rows fail)
+// 0: the VALU pass for at most AUTO_SMALL_ROWS selection rows (none), MFMA otherwise; 1:
+// always MFMA; 2: always VALU (calls with more than SMALL_ROWS rows fail)
 static std::atomic<int> g_score_path{0};
 
 extern "C" int ma_prefix_scores_path(int mode) {
@@ -1203,8 +1205,6 @@ static int prefix_scores(const char *who, ma_tensor4 q, int B, int Hq, int T, in
                      R2);
         return MA_EUNSUPPORTED;
     }
-    // (auto: up to AUTO_SMALL_ROWS rows, where it measured at least as fast as the padded
-    // MFMA pass at config 2's prefix; at 14 rows the dot products make it VALU-bound)
     if (path == 2 || (path == 0 && R2 <= AUTO_SMALL_ROWS)) {
         const int units = (n + UNIT - 1) / UNIT;
         // about 8 waves per CU in all, each on a contiguous run of units

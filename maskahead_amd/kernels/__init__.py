@@ -11,6 +11,7 @@ from .ops import (
 )
 from .select import prefix_scores_topk, topk_ascending
 from .splitk import Prefix, dequantize_prefix, prefix_scores, splitk_attention
+from .step0 import Step0Buffers, step0_select
 
 __all__ = [
     "KernelUnavailableError",
@@ -25,5 +26,7 @@ __all__ = [
     "quantize_values_into",
     "selector_topk",
     "splitk_attention",
+    "Step0Buffers",
+    "step0_select",
     "topk_ascending",
 ]

@@ -1,0 +1,105 @@
+"""Step 0 of a sparse layer in one library call (the reference session's _fast_step0,
+session.py:1403-1454): split-K attention with the prefix statistics, the value-aware
+prefix scores, the read-set top-k (ascending indices) and the gather of the selected
+entries, enqueued by ``ma_step0`` -- the same launches and results as splitk_attention +
+prefix_scores_topk + gather_packed_kv, without the per-op Python, ctypes packing and
+allocation.  ``Step0Buffers`` holds one layer's outputs and workspace between calls, so
+a call allocates nothing once its buffers have grown to the layer's sizes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _native as N
+from .select import _state
+from .splitk import Prefix
+
+
+def _vround(prefix: Prefix, r: int, query: torch.Tensor) -> int:
+    """The dtype the reference reads a long packed prefix through (splitk.py:513-516), as
+    splitk_attention records it in its statistics."""
+    if prefix.nq and (r > 256 or prefix.n > 256) and query.dtype != torch.float32:
+        return N.dtype_code(query.dtype)
+    return 0
+
+
+class Step0Buffers:
+    """One layer's step-0 outputs and workspace, grown to fit and reused: out [B, Hq, T, D]
+    (query dtype), M_p / L_p [B, Hkv, R] f32, O_p [B, Hkv, R, D], mass / score [B, Hkv, n]
+    f32, idx [B, Hkv, k] int64 (views into storage of the largest sizes seen).  A later
+    call of the same layer overwrites them."""
+
+    def __init__(self):
+        self._store: dict = {}
+
+    def take(self, name: str, numel: int, dtype: torch.dtype, device: torch.device, shape: tuple) -> torch.Tensor:
+        t = self._store.get(name)
+        if t is None or t.numel() < numel or t.dtype != dtype or t.device != device:
+            t = torch.empty((max(numel, 1),), dtype=dtype, device=device)
+            self._store[name] = t
+        return t[:numel].view(shape)
+
+
+def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, current_key: torch.Tensor,
+                 current_value: torch.Tensor, rows, k: int, *, value: bool, scaling: float | None = None,
+                 out_key: torch.Tensor | None = None, out_value: torch.Tensor | None = None,
+                 workspace: Step0Buffers | None = None):
+    """(out, (M_p, L_p, O_p, prefix_used), mass, score, idx) of one step 0, in one library
+    call.  rows: the selection rows (a host list -- 0 .. T2-1 in order needs no table --
+    or an int32 device tensor).  out_key / out_value (optional): [B, Hkv, k, D] views the
+    selected entries are gathered into (the layer's compact buffer).  workspace: where the
+    scratch workspace lives (default bufs); layers run one after another on a stream can
+    share one."""
+    if query.ndim != 4 or current_key.ndim != 4:
+        raise ValueError("query and current_key must be [B, H, T, D]")
+    N.require_gpu(query, "query")
+    b, hq, t, d = query.shape
+    hkv = current_key.shape[1]
+    if hq % hkv:
+        raise ValueError("Hq must be divisible by Hkv")
+    r = (hq // hkv) * t
+    n = prefix.n
+    k = int(k)
+    if n <= 0 or not 0 < k <= n:
+        raise ValueError(f"read budget k={k} outside [1, {n}]")
+    prefix.check_mask(b, hkv)
+    if isinstance(rows, torch.Tensor) and rows.is_cuda:
+        q_rows = rows.to(torch.int32).contiguous()
+        t2 = int(q_rows.numel())
+    else:
+        host = tuple(int(x) for x in (rows.tolist() if isinstance(rows, torch.Tensor) else rows))
+        if any(x < 0 or x >= t for x in host):
+            raise ValueError(f"q_rows must be block positions in [0, {t})")
+        from .splitk import _row_table
+
+        q_rows = None if host == tuple(range(len(host))) else _row_table(host, query.device)
+        t2 = len(host)
+    if t2 == 0:
+        raise ValueError("q_rows cannot be empty")
+    dev = query.device
+    nat = prefix.native()
+    vround = _vround(prefix, r, query)
+    used = prefix.with_vround(vround) if vround else prefix
+    out = bufs.take("out", query.numel(), query.dtype, dev, tuple(query.shape))
+    mp = bufs.take("mp", b * hkv * r, torch.float32, dev, (b, hkv, r))
+    lp = bufs.take("lp", b * hkv * r, torch.float32, dev, (b, hkv, r))
+    op = bufs.take("op", b * hkv * r * d, query.dtype, dev, (b, hkv, r, d))
+    mass = bufs.take("mass", b * hkv * n, torch.float32, dev, (b, hkv, n))
+    score = bufs.take("score", b * hkv * n, torch.float32, dev, (b, hkv, n)) if value else None
+    idx = bufs.take("idx", b * hkv * k, torch.int64, dev, (b, hkv, k))
+    ws_bytes = N.size_query("ma_step0_workspace_bytes", b, hkv, hq, t, d, prefix.nq, prefix.nf)
+    if ws_bytes <= 0:
+        raise N.KernelUnavailableError(f"ma_step0: no workspace size for n={n}")
+    ws = (workspace or bufs).take("ws", ws_bytes, torch.uint8, dev, (ws_bytes,))
+    stream = N.stream_of(query)
+    st = _state(dev, N.size_query("ma_topk_state_bytes", b * hkv), stream)
+    scale = float(scaling) if scaling is not None else d ** -0.5
+    tc = current_key.shape[2]
+    rc = N.load().ma_step0(
+        N.t4(query), b, hq, t, d, nat, hkv, N.t4(current_key if tc else None), N.t4(current_value if tc else None),
+        tc, scale, N.t4(out), mp.data_ptr(), lp.data_ptr(), op.data_ptr(), N.ptr(q_rows), t2, 1 if value else 0,
+        2 if value else 1, vround, mass.data_ptr(), N.ptr(score), k, idx.data_ptr(), N.t4(out_key),
+        N.t4(out_value), st.data_ptr(), st.numel(), ws.data_ptr(), ws_bytes, stream)
+    N.check(rc, "ma_step0")
+    return out, (mp, lp, op, used), mass, score, idx

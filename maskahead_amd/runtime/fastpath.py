@@ -25,9 +25,8 @@ from dataclasses import dataclass, field
 import torch
 
 from .._native import KernelUnavailableError
-from ..kernels.ops import gather_packed_kv
-from ..kernels.select import prefix_scores_topk
 from ..kernels.splitk import Prefix, prefix_scores, splitk_attention
+from ..kernels.step0 import Step0Buffers, step0_select
 
 
 def fast_path_supported(config, head_dim: int, device_type: str = "cuda"):
@@ -117,6 +116,8 @@ class FastLayerPath:
     _prefix_cache: dict = field(default_factory=dict)
     _compact_prefix: dict = field(default_factory=dict)
     _planes_generation: int = -1
+    _step0_bufs: dict = field(default_factory=dict)
+    _step0_ws: Step0Buffers = field(default_factory=Step0Buffers)
 
     @property
     def head_dim(self) -> int:
@@ -240,32 +241,33 @@ class FastLayerPath:
         if prefix.n == 0:
             return self.current_only(query, current_key, current_value, 0, 0)
         scale = self.head_dim ** -0.5
-        out, stats = splitk_attention(query, prefix, current_key, current_value, scaling=scale,
-                                      want_prefix=need_sel or need_mass)
-        if not (need_sel or need_mass):
-            return out
-        rows = self.rows(self.query_indices)
-        value = need_sel and self.value_aware
         if need_sel:
+            # the whole step in one library call, into this layer's reused buffers (valid
+            # until the layer's next step 0)
             k = min(int(topk), prefix.n)
             if k <= 0:
                 raise ValueError("the read budget must be positive")
             if not self.sort_indices:
                 raise KernelUnavailableError("the HIP read-set select returns ascending indices only "
                                              "(selector.sort_indices = False is not built)")
-            # the score pass builds the select's first histogram level (one launch less)
-            mass, score, idx = prefix_scores_topk(query, prefix, stats, rows, k, value=value,
-                                                  rank="score" if value else "mass", scaling=scale)
-        else:
-            mass, score = prefix_scores(query, prefix, stats, rows, value=value, scaling=scale)
-        if need_mass:
-            self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
-        if need_sel:
             state = self.ensure_state(layer_idx, k)
-            gather_packed_kv(prefix, idx, dtype=self.compute_dtype,
-                             out_key=state.key[:, :, :k, :], out_value=state.value[:, :, :k, :])
+            bufs = self._step0_bufs.setdefault(layer_idx, Step0Buffers())
+            out, _, mass, _, idx = step0_select(bufs, query, prefix, current_key, current_value,
+                                                self.rows(self.query_indices), k, value=self.value_aware,
+                                                scaling=scale, out_key=state.key[:, :, :k, :],
+                                                out_value=state.value[:, :, :k, :], workspace=self._step0_ws)
+            if need_mass:
+                self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
             state.indices = idx
             state.selected_k = k
+            return out
+        out, stats = splitk_attention(query, prefix, current_key, current_value, scaling=scale,
+                                      want_prefix=need_mass)
+        if not need_mass:
+            return out
+        # a dense layer that keeps its prefix mass (eviction input)
+        mass, _ = prefix_scores(query, prefix, stats, self.rows(self.query_indices), value=False, scaling=scale)
+        self.last_mass[layer_idx] = mass if live_slots is None else mass.gather(-1, live_slots.to(torch.int64))
         return out
 
     def compact_attention(self, layer_idx, query, current_key, current_value):
