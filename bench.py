@@ -40,8 +40,8 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
-PASS1_KERNEL = "splitk_fwd_kernel<128, 0>"     # packed-source split-K pass 1 (carries the current block)
-SCORE_KERNEL = "score_kernel<128, 0, 1, 1024>"  # value-aware score pass over packed K/V
+PASS1_KERNEL = "splitk_fwd_kernel<128, 0, true>"  # packed-source split-K pass 1, whole tiles (carries the current block)
+SCORE_KERNEL = "score_kernel<128, 0, 1, 1024, false, true>"  # value-aware score pass over packed K/V
 
 
 def parse():

@@ -14,7 +14,6 @@
 //                into the third K / V buffer, then issue the loads of tile i+3.
 // Pass 2 (splitk_combine_kernel): log-sum-exp merge of the partials into the output and
 // the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
-// the prefix-only statistics (M_p, L_p, O_p) of splitk.py:272-318.
 #include <mutex>
 #include <type_traits>
 
