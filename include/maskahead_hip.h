@@ -239,6 +239,16 @@ int64_t ma_value_score_workspace_bytes(int rows, int n, int D);
 int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, int B, int H, int n, int D, int fp32_mode,
                    float *score, int64_t score_stride, void *workspace, int64_t workspace_bytes,
                    void *stream);
+/* value score over a cache's live slots (the lookahead keep score of session.py:1995-2025:
+ * value_score(a, live_values) with live_values = session.py:263-268): entry j of lane
+ * (b, h) is slot slots[(b*H + h)*slot_stride + j] of the cache lane described by p, its
+ * value dequantized (packed slots < p->nq) or read (16-bit rows) and rounded to vdtype
+ * exactly as ma_gather_kv writes it; the scores equal ma_gather_kv + ma_value_score on
+ * those rows, bit for bit, without the gathered [n, D] rows.  Slots outside the cache give
+ * zero rows.  D 64 or 128; workspace ma_value_score_workspace_bytes(B*H, n, D). */
+int ma_value_score_slots(const float *a, int64_t a_stride, const ma_prefix *p, const int32_t *slots,
+                         int64_t slot_stride, int B, int H, int n, int D, int vdtype, int fp32_mode, float *score,
+                         int64_t score_stride, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* compaction of survivors (PackedKVCache.compact, cache.py:342-367; compact_tokens,
  * cache.py:659-678; EvictionState.compact, eviction.py:411-418): for every lane (b, h) and

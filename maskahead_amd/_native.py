@@ -81,6 +81,7 @@ SIGNATURES = {
                             _P, _I64, _P, _I64, _P]),
     "ma_value_score_workspace_bytes": (_I64, [_I, _I, _I]),
     "ma_value_score": (_I, [_P, _I64, _T4, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P]),
+    "ma_value_score_slots": (_I, [_P, _I64, _PREF, _P, _I64, _I, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P]),
     "ma_compact_workspace_bytes": (_I64, [_I, _I, _P, _I]),
     "ma_compact_tokens": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _I64P, _I, _P, _I64, _P]),
     "ma_append_tokens": (_I, [_T4, _T4, _I, _I, _I, _I, _I, _P]),

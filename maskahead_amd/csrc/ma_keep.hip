@@ -12,6 +12,11 @@
 //   Three launches: per-chunk partial sums (grid chunks x rows, chunks of 256 entries),
 //   the centre per row, the per-entry distances and scores (grid chunks x rows).  Fixed
 //   summation order: results are deterministic.
+//   Slot form (ma_value_score_slots): v_j is the value of slot slots[row, j] of a cache
+//   lane, dequantized and rounded to the compute dtype exactly as ma_gather_kv writes it
+//   (the reference's live_values, session.py:263-268), read straight from the packed codes
+//   or the 16-bit rows: the same scores as ma_gather_kv + ma_value_score, without writing
+//   and re-reading the gathered [live, D] rows.
 //
 // compaction (cache.py:342-367 / 659-678, eviction.py:411-418): dst[i] = src[keep[i]] for
 //   i < C, in place, for several token-major planes of one lane at once (bf16 K and V,
@@ -48,6 +53,17 @@ struct VsArgs {
     const void *v;        // [B, H, n, D] (strides b, h, n in elements), dtype vdtype
     int64_t sa, sv0, sv1, sv2;
     int H, n, D, vdtype, fp32_mode, chunk;
+    // slot form: entry j of row (b, h) is slot slots[row * sslot + j] of lane (b, h) of a
+    // cache whose slots [0, nq) are packed (value codes vq [B, H, nq, D/32, 16] u8, scale /
+    // zero vs, vz [B, H, nq, D/32] f16) and [nq, nq + nf) 16-bit rows vf (dtype fdtype);
+    // values rounded to vdtype, as the gather writes them; slots outside [0, nq + nf) are 0
+    const int32_t *slots;
+    int64_t sslot;
+    const uint8_t *vq;
+    const uint16_t *vsc, *vzp;
+    const void *vf;
+    int64_t svq[4], svs[3], svf[3];
+    int nq, nf, fdtype;
     double *part;         // [rows, nchunks, D + 1]
     float *centre;        // [rows, D]
     float *score;         // [rows, n] (row stride ss)
@@ -82,7 +98,44 @@ __device__ __forceinline__ void load8(const char *p, int c0, int dtype, float (&
     }
 }
 
+__device__ __forceinline__ float round_to(float x, int dtype) {
+    if (dtype == MA_BF16) return ma_round_bf16(x);
+    if (dtype == MA_F16) return ma_round_f16(x);
+    return x;
+}
+
+// 8 channels [c0, c0+8) of entry j of a row: a dense row, or (SLOTS) the value of the
+// entry's cache slot as ma_gather_kv writes it in dtype vdtype
+template <bool SLOTS>
+__device__ __forceinline__ void entry8(const VsArgs &a, int row, int j, int c0, float (&x)[8]) {
+    if constexpr (!SLOTS) {
+        load8(vrow(a, row, j), c0, a.vdtype, x);
+    } else {
+        const int b = row / a.H, h = row % a.H;
+        const int s = a.slots[(int64_t)row * a.sslot + j];
+        if (s >= 0 && s < a.nq) {
+            const int cg = c0 / 32;
+            const uint32_t w = *(const uint32_t *)(a.vq + b * a.svq[0] + h * a.svq[1] + (int64_t)s * a.svq[2] +
+                                                   cg * a.svq[3] + (c0 % 32) / 2);
+            const int64_t so = b * a.svs[0] + h * a.svs[1] + (int64_t)s * a.svs[2] + cg;
+            const float sc = ma_f16_to_f32(a.vsc[so]), ze = ma_f16_to_f32(a.vzp[so]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = round_to(ma_dq((w >> (4 * i)) & 15u, sc, ze), a.vdtype);
+        } else if (s >= a.nq && s < a.nq + a.nf) {
+            const char *p = (const char *)a.vf +
+                            (b * a.svf[0] + h * a.svf[1] + (int64_t)(s - a.nq) * a.svf[2]) * (a.fdtype == MA_F32 ? 4 : 2);
+            load8(p, c0, a.fdtype, x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = round_to(x[i], a.vdtype);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = 0.f;
+        }
+    }
+}
+
 // grid (nchunks, rows), 256 threads = 16 token lanes x 16 channel octets (D <= 128).
+template <bool SLOTS>
 __global__ void __launch_bounds__(VS_NT) vs_partial_kernel(VsArgs a) {
     __shared__ double red[VS_TOK][129];
     const int chunk = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
@@ -104,7 +157,7 @@ __global__ void __launch_bounds__(VS_NT) vs_partial_kernel(VsArgs a) {
             const bool ok = j < j1;
             const int jl = ok ? j : j0;
             aw[u] = ok ? ar[jl] : 0.f;
-            if (cok) load8(vrow(a, row, jl), c0, a.vdtype, x[u]);
+            if (cok) entry8<SLOTS>(a, row, jl, c0, x[u]);
         }
 #pragma unroll
         for (int u = 0; u < VS_BATCH; ++u) {
@@ -177,8 +230,9 @@ __global__ void __launch_bounds__(VC_NT) vs_centre_kernel(VsArgs a) {
     a.centre[(int64_t)row * a.D + tid] = cen;
 }
 
-// grid (nchunks, rows), 256 threads: one 16-channel slice of one entry per thread pair...
-// here: 16 lanes per entry (8 channels each), 16 entries per step.
+// grid (nchunks, rows), 256 threads: 16 lanes per entry (8 channels each), 16 entries per
+// step.
+template <bool SLOTS>
 __global__ void __launch_bounds__(VS_NT) vs_score_kernel(VsArgs a) {
     __shared__ float cen[128];
     const int chunk = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
@@ -200,7 +254,7 @@ __global__ void __launch_bounds__(VS_NT) vs_score_kernel(VsArgs a) {
         for (int u = 0; u < VS_BATCH; ++u) {
             const int j = jb0 + u * VS_TOK + tl;
             const int jl = j < j1 ? j : j0;
-            if (cok) load8(vrow(a, row, jl), c0, a.vdtype, x[u]);
+            if (cok) entry8<SLOTS>(a, row, jl, c0, x[u]);
             aw[u] = ar[jl];
         }
 #pragma unroll
@@ -371,11 +425,78 @@ extern "C" int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, in
     va.centre = (float *)(va.part + (int64_t)rows * va.nchunks * (D + 1));
     va.score = score;
     va.ss = score_stride;
+    va.slots = nullptr;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid(va.nchunks, rows);
-    hipLaunchKernelGGL(vs_partial_kernel, grid, dim3(VS_NT), 0, st, va);
+    hipLaunchKernelGGL(vs_partial_kernel<false>, grid, dim3(VS_NT), 0, st, va);
     hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
-    hipLaunchKernelGGL(vs_score_kernel, grid, dim3(VS_NT), 0, st, va);
+    hipLaunchKernelGGL(vs_score_kernel<false>, grid, dim3(VS_NT), 0, st, va);
+    return ma_check_launch(who);
+}
+
+int ma_validate_prefix(const ma_prefix *p, int D, const char *who);
+
+extern "C" int ma_value_score_slots(const float *a, int64_t a_stride, const ma_prefix *p, const int32_t *slots,
+                                    int64_t slot_stride, int B, int H, int n, int D, int vdtype, int fp32_mode,
+                                    float *score, int64_t score_stride, void *workspace, int64_t workspace_bytes,
+                                    void *stream) {
+    const char *who = "ma_value_score_slots";
+    int rc = ma_validate_prefix(p, D, who);
+    if (rc) return rc;
+    if (!a || !slots || !score || B <= 0 || H <= 0 || n < 0 || D <= 0 || D > 128 || D % 32 || a_stride < n ||
+        score_stride < n || slot_stride < n || (vdtype != MA_BF16 && vdtype != MA_F16 && vdtype != MA_F32) ||
+        (p->nq > 0 && (p->vbits != 4 || p->vgroup != 32))) {
+        ma_set_error("%s: bad arguments (B=%d H=%d n=%d D=%d)", who, B, H, n, D);
+        return MA_EINVAL;
+    }
+    if (p->nq > 0 && ((p->svq[0] | p->svq[1]) & 3)) {
+        ma_set_error("%s: value code strides must be multiples of 4 bytes", who);
+        return MA_EINVAL;
+    }
+    if (p->nf > 0 && (((uintptr_t)p->vf & 15) || p->svf[0] % 8 || p->svf[1] % 8 || p->svf[2] % 8)) {
+        ma_set_error("%s: 16-bit rows must be 16-byte aligned with aligned row strides", who);
+        return MA_EINVAL;
+    }
+    const int rows = B * H;
+    const int64_t need = ma_value_score_workspace_bytes(rows, n, D);
+    if (!workspace || workspace_bytes < need) {
+        ma_set_error("%s: workspace %lld bytes < %lld needed", who, (long long)workspace_bytes, (long long)need);
+        return MA_EWORKSPACE;
+    }
+    if (n == 0) return MA_OK;
+    VsArgs va = VsArgs{};
+    va.a = a;
+    va.sa = a_stride;
+    va.H = H;
+    va.n = n;
+    va.D = D;
+    va.vdtype = vdtype;
+    va.fp32_mode = fp32_mode;
+    va.chunk = VS_CHUNK;
+    va.nchunks = (n + va.chunk - 1) / va.chunk;
+    va.part = (double *)(((uintptr_t)workspace + 15) & ~(uintptr_t)15);
+    va.centre = (float *)(va.part + (int64_t)rows * va.nchunks * (D + 1));
+    va.score = score;
+    va.ss = score_stride;
+    va.slots = slots;
+    va.sslot = slot_stride;
+    va.vq = (const uint8_t *)p->vq;
+    va.vsc = (const uint16_t *)p->vs;
+    va.vzp = (const uint16_t *)p->vz;
+    va.vf = p->vf;
+    for (int i = 0; i < 4; ++i) va.svq[i] = p->svq[i];
+    for (int i = 0; i < 3; ++i) {
+        va.svs[i] = p->svs[i];
+        va.svf[i] = p->svf[i];
+    }
+    va.nq = p->nq;
+    va.nf = p->nf;
+    va.fdtype = p->fdtype;
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid(va.nchunks, rows);
+    hipLaunchKernelGGL(vs_partial_kernel<true>, grid, dim3(VS_NT), 0, st, va);
+    hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
+    hipLaunchKernelGGL(vs_score_kernel<true>, grid, dim3(VS_NT), 0, st, va);
     return ma_check_launch(who);
 }
 

@@ -2,7 +2,7 @@
 compaction of survivors and the append of a finalized block.
 
 Host side of the gfx950 kernels behind ``ma_keep_select``, ``ma_value_score``,
-``ma_compact_tokens`` and ``ma_append_tokens``.  They replace the torch ops the
+``ma_value_score_slots``, ``ma_compact_tokens`` and ``ma_append_tokens``.  They replace the torch ops the
 reference runs on the keep path: ``EvictionState.survivors`` (eviction.py:325-409),
 ``value_score`` (runtime/session.py:27-40), the gathers of ``PackedKVCache.compact``
 (cache.py:342-367), ``compact_tokens`` (cache.py:659-678) and ``EvictionState.compact``
@@ -123,6 +123,54 @@ def value_score(a: torch.Tensor, v: torch.Tensor, *, fp32: bool | None = None, o
                             o2.data_ptr(), o2.stride(0) if rows > 1 else n, ws.data_ptr(), ws.numel(),
                             N.stream_of(v))
     N.check(rc, "ma_value_score")
+    return out
+
+
+def value_score_slots(a: torch.Tensor, prefix, slots: torch.Tensor, *, dtype: torch.dtype = torch.bfloat16,
+                      fp32: bool | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """value_score(a, v) where v[b, h, j] is the value of cache slot slots[b, h, j] of lane
+    (b, h) of the cache lanes `prefix` (a kernels.splitk.Prefix) describes, as
+    gather_packed_kv(prefix, slots, dtype=dtype) returns it: the lookahead keep score over
+    the live entries (runtime/session.py: value_score(a, live_values(...)),
+    session.py:263-268, 1995-2025) computed from the packed codes or 16-bit rows directly,
+    bit for bit the same, without the gathered [B, H, n, D] rows.
+
+    a f32 [B, H, n]; slots int32 [B, H, >= n] (entries contiguous, lanes uniformly
+    strided, e.g. the eviction state's phys[layer]); returns f32 [B, H, n]."""
+    from .splitk import Prefix
+
+    if not isinstance(prefix, Prefix):
+        raise TypeError("prefix must be a kernels.splitk.Prefix")
+    N.require_gpu(a, "a")
+    if fp32 is None:
+        fp32 = os.environ.get("BITSIEVE_VSCORE_FP32") == "1"
+    if a.dtype != torch.float32 or a.dim() != 3:
+        raise ValueError("a must be float32 [B, H, n]")
+    if slots.dtype != torch.int32 or slots.dim() != 3 or tuple(slots.shape[:2]) != tuple(a.shape[:2]):
+        raise ValueError("slots must be int32 [B, H, >= n] matching a")
+    b, h, n = a.shape
+    if slots.shape[2] < n:
+        raise ValueError(f"slots hold {slots.shape[2]} entries per lane, {n} needed")
+    s2 = slots[..., :n]
+    if s2.stride(-1) != 1 or (b > 1 and s2.stride(0) != h * s2.stride(1)):
+        s2 = s2.contiguous()
+    sstride = s2.stride(1) if h > 1 else (s2.stride(0) if b > 1 else n)
+    a2 = a if a.is_contiguous() else a.contiguous()
+    if out is None:
+        out = torch.empty((b, h, n), device=a.device, dtype=torch.float32)
+    if n == 0:
+        return out
+    src = prefix.kq if prefix.nq else prefix.kf
+    d = int(src.shape[-2] if prefix.nq else src.shape[-1])
+    lib = N.load()
+    ws_bytes = int(lib.ma_value_score_workspace_bytes(b * h, n, d))
+    if ws_bytes < 0:
+        raise N.KernelUnavailableError(f"value_score_slots: head_dim {d} not built")
+    ws = torch.empty((ws_bytes,), device=a.device, dtype=torch.uint8)
+    rc = lib.ma_value_score_slots(a2.data_ptr(), n, prefix.native(), s2.data_ptr(), sstride, b, h, n, d,
+                                  N.dtype_code(dtype), 1 if fp32 else 0, out.data_ptr(), n, ws.data_ptr(), ws.numel(),
+                                  N.stream_of(a))
+    N.check(rc, "ma_value_score_slots")
     return out
 
 

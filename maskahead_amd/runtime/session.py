@@ -115,6 +115,9 @@ def lookahead_scores(cache, state, a1: dict, a_probe: dict | None = None, *, use
     (session.py:1995-2025): a = the step-0 mass of the block's own queries (a1[layer],
     live order) + the probe mass of the next blocks (a_probe[layer], when probed); the
     score is value_score(a, v_live) (lookahead_score "value") or a itself ("mass")."""
+    from ..kernels.keep import value_score_slots
+    from ..kernels.splitk import Prefix
+
     L = state.num_layers
     score = torch.empty((L, cache.batch_size, cache.num_kv_heads, state.live), dtype=torch.float32,
                         device=cache.device)
@@ -122,7 +125,13 @@ def lookahead_scores(cache, state, a1: dict, a_probe: dict | None = None, *, use
         a = a1[layer]
         if a_probe is not None and layer in a_probe:
             a = a + a_probe[layer]
-        score[layer] = value_score(a, live_values(cache, state, layer)) if use_value else a
+        if use_value:
+            # value_score(a, live_values(cache, state, layer)), from the cache's codes
+            # directly (the same bits, no gathered [B, Hkv, live, D] rows)
+            value_score_slots(a.contiguous(), Prefix.from_view(cache.layer_view(layer)),
+                              state.phys[layer, ..., :state.live], dtype=cache.compute_dtype, out=score[layer])
+        else:
+            score[layer] = a
     return score
 
 

@@ -10,7 +10,8 @@ import pytest
 import torch
 
 from maskahead_amd.eviction import EvictionConfig, EvictionState
-from maskahead_amd.kernels.keep import append_tokens, compact_tokens, keep_select, value_score
+from maskahead_amd.kernels import gather_packed_kv
+from maskahead_amd.kernels.keep import append_tokens, compact_tokens, keep_select, value_score, value_score_slots
 from oracle import attention as OA
 from oracle import codec as OC
 from oracle import selection as OS
@@ -117,6 +118,43 @@ def test_value_score_fp32_branch(gpu):
     got = value_score(a.to(gpu), v.to(gpu), fp32=True).cpu()
     want = OA.value_score_fp32(a, v)
     assert torch.allclose(got, want, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("d,dtype,fp32", [(128, torch.bfloat16, False), (64, torch.bfloat16, False),
+                                           (128, torch.float32, False), (128, torch.bfloat16, True)])
+def test_value_score_slots_equals_gather_then_score(gpu, d, dtype, fp32):
+    """The lookahead keep score straight from a cache's slots (ma_value_score_slots) is the
+    value score of the rows gather_packed_kv returns for those slots, bit for bit: packed
+    slots, 16-bit residual slots, slots outside the cache (zero rows), capacity-strided
+    slot rows; and, in the bf16 branch, the oracle's value score of the oracle's dequant."""
+    from _util import dequant_cpu, gpu_prefix, layer_inputs, packed_cpu
+
+    n, tail = 640, 72
+    _, k, v, _, _ = layer_inputs(hq=4, hkv=2, d=d, n=n + tail, t=4, seed=41, dtype=torch.bfloat16)
+    store, nq = packed_cpu(k[:, :, :n], v[:, :, :n], pad_groups=2, pad_tokens=50)
+    p = gpu_prefix(store, nq, gpu, kf=k[:, :, n:], vf=v[:, :, n:])
+    g = torch.Generator().manual_seed(d)
+    live, cap = 500, 530
+    slots = torch.full((1, 2, cap), -7, dtype=torch.int32)
+    for h in range(2):
+        slots[0, h, :live] = torch.randperm(n + tail, generator=g)[:live].sort().values.to(torch.int32)
+    slots[0, 1, 17] = -1                       # outside the cache: a zero row
+    slots[0, 0, 33] = n + tail + 5
+    a = torch.rand((1, 2, live), generator=g)
+    a[..., ::9] = 0.0
+    ag, sg = a.to(gpu), slots.to(gpu)
+    got = value_score_slots(ag, p, sg, dtype=dtype, fp32=fp32)
+    _, vg = gather_packed_kv(p, sg[..., :live].to(torch.int64), dtype=dtype)
+    want = value_score(ag, vg, fp32=fp32)
+    assert torch.equal(got.cpu(), want.cpu())
+    if dtype == torch.bfloat16 and not fp32:
+        kd, vd = dequant_cpu(store, nq)
+        v_all = torch.cat([vd.to(torch.bfloat16), v[:, :, n:]], 2)
+        idx = slots[..., :live].to(torch.int64)
+        ok = (idx >= 0) & (idx < n + tail)
+        rows = torch.gather(v_all, 2, idx.clamp(0, n + tail - 1).unsqueeze(-1).expand(-1, -1, -1, d))
+        rows = torch.where(ok.unsqueeze(-1), rows, torch.zeros((), dtype=rows.dtype))
+        assert torch.equal(got.cpu(), OA.value_score_bf16(a, rows))
 
 
 @pytest.mark.parametrize("kind", ["survivors", "arbitrary"])
