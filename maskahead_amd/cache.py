@@ -139,6 +139,7 @@ class PackedKVCache:
         # bumped whenever the planes are replaced (growth, shrink after compaction): holders
         # of views or descriptors of the planes drop them when it changes
         self.planes_generation = 0
+        self._pending_rebuild_status: torch.Tensor | None = None   # a rebuild's unread errors
         for name in _UNITS:
             setattr(self, name, None)
         gk = quant.key_token_group
@@ -453,14 +454,27 @@ class PackedKVCache:
         [L, B, H, old length]: the new slot of every old slot, -1 if dropped."""
         return self._rebuild(groups_before, encode, groups_after, stage)
 
+    def check_rebuild(self) -> None:
+        """Raise the errors of a rebuild run with check=False (see _rebuild), if any; one
+        small copy to the host.  A no-op when none is pending."""
+        from .kernels.rebuild import raise_rebuild_status
+
+        status, self._pending_rebuild_status = self._pending_rebuild_status, None
+        if status is not None:
+            raise_rebuild_status(status)
+
     def _rebuild(self, groups_before, encode, groups_after, stage, phys: torch.Tensor | None = None,
-                 live: int = 0) -> torch.Tensor:
+                 live: int = 0, check: bool = True) -> torch.Tensor:
         """rebuild(), with the eviction state's slots phys (int32 [L, B, H, capacity]) rewritten
         through the remap in the same launch.  New planes are allocated and written by
         ma_rebuild_packed over every layer at once (the lanes of all layers folded into the
-        batch axis); the old ones are dropped."""
+        batch axis); the old ones are dropped.  check=False leaves the launch's error status
+        on the device, to be raised by check_rebuild() -- called by the next rebuild -- instead
+        of reading it back now."""
         from .kernels.rebuild import rebuild_packed
         from .kernels.splitk import Prefix
+
+        self.check_rebuild()
 
         if self._append_plan is not None:
             raise RuntimeError("rebuild during an append")
@@ -489,9 +503,11 @@ class PackedKVCache:
                           vz=f("v_zero"), kf=f("k_residual"), vf=f("v_residual"), nq=nq, nf=nf, kb=4, vb=4)
 
         new_planes = {name: getattr(self, name) for name in self._planes}
-        rebuild_packed(prefix(old_planes, old_q, old_r), prefix(new_planes, ql, st), B=lead[0] * lead[1], H=lead[2],
-                       D=self.head_dim, groups_before=groups_before, encode=encode, groups_after=groups_after,
-                       stage=stage, remap=remap, phys=phys, live=live)
+        status = rebuild_packed(prefix(old_planes, old_q, old_r), prefix(new_planes, ql, st), B=lead[0] * lead[1],
+                                H=lead[2], D=self.head_dim, groups_before=groups_before, encode=encode,
+                                groups_after=groups_after, stage=stage, remap=remap, phys=phys, live=live,
+                                check=check)
+        self._pending_rebuild_status = status
         self.length, self.quantized_length, self.residual_length = ql + st, ql, st
         self.dropped += old_len - self.length
         self._note_peak()

@@ -409,59 +409,71 @@ __device__ void copy_group(const RbArgs &a, const LaneStore &o, const LaneStore 
 
 // New group g1 + j of a lane: the 32 old entries encode[32 j ..] (zeros past the list or
 // for padding) dequantized to bf16 and quantized again in bf16 arithmetic
-// (quantize_key_groups_into / quantize_values_into on the gathered bf16 rows).
+// (quantize_key_groups_into / quantize_values_into on the gathered bf16 rows).  Item (t,
+// octet o) = channels 8o .. 8o+7 of entry t, one or two per thread.  A value group (32
+// channels of one entry) is the items of 4 adjacent lanes: its range comes from two lane
+// exchanges and each lane quantizes its 8 channels in registers.  Keys go through LDS
+// (one column per channel) and are quantized by P = 256 / D adjacent lanes per channel,
+// 32 / P tokens each, their ranges combined the same way.
 __device__ void encode_group(const RbArgs &a, const LaneStore &o, const LaneStore &n, int lane, int j) {
     __shared__ float xk[KG][129];   // head_dim <= 128 (+1: column reads across rows)
-    __shared__ float xv[KG][129];
-    const int tid = threadIdx.x, D = a.D, ncg = D / VG, oct = D / 8;
+    const int tid = threadIdx.x, D = a.D, oct = D / 8;
+    const int g = a.g1 + j;
     for (int u = tid; u < KG * oct; u += RB_THREADS) {
-        const int t = u / oct, d0 = (u % oct) * 8;
+        const int t = u / oct, oc = u % oct, d0 = oc * 8;
         const int64_t src = list_at(a.enc, a.senc, lane, a.m, j * KG + t);
         float k8[8], v8[8];
         old_entry8(a, o, src, d0, k8, v8);
 #pragma unroll
+        for (int i = 0; i < 8; ++i) xk[t][d0 + i] = k8[i];
+        // the value group of channels 32 c .. 32 c + 31: lanes with octets 4c .. 4c + 3 (oct
+        // is a multiple of 4 and divides 64, so they are adjacent lanes of one wave)
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
         for (int i = 0; i < 8; ++i) {
-            xk[t][d0 + i] = k8[i];
-            xv[t][d0 + i] = v8[i];
+            lo = fminf(lo, v8[i]);
+            hi = fmaxf(hi, v8[i]);
+        }
+        lo = fminf(lo, __shfl_xor(lo, 1));
+        hi = fmaxf(hi, __shfl_xor(hi, 1));
+        lo = fminf(lo, __shfl_xor(lo, 2));
+        hi = fmaxf(hi, __shfl_xor(hi, 2));
+        const QuantGroup qp = quant_params(lo, hi, MA_BF16);
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w |= quant_code(v8[i], qp, MA_BF16) << (i * 4);
+        const int c = d0 / VG, q = (d0 % VG) / 8;
+        const int64_t tok = (int64_t)g * KG + t;
+        *(uint32_t *)(n.vq + tok * n.vq_n + c * n.vq_c + q * 4) = w;
+        if (q == 0) {
+            const _Float16 s16 = (_Float16)qp.step, z16 = (_Float16)qp.lo;
+            n.vs[tok * n.vs_n + c] = *(const uint16_t *)&s16;
+            n.vz[tok * n.vs_n + c] = *(const uint16_t *)&z16;
         }
     }
     __syncthreads();
-    const int g = a.g1 + j;
-    // keys: one channel over the group's 32 tokens
-    for (int d = tid; d < D; d += RB_THREADS) {
-        float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < KG; ++t) {
-            lo = fminf(lo, xk[t][d]);
-            hi = fmaxf(hi, xk[t][d]);
-        }
-        const QuantGroup qp = quant_params(lo, hi, MA_BF16);
-        uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int t = 0; t < KG; ++t) w[t >> 3] |= quant_code(xk[t][d], qp, MA_BF16) << ((t & 7) * 4);
-        *(uint4 *)(n.kq + (int64_t)g * n.kq_g + d * n.kq_d) = uint4{w[0], w[1], w[2], w[3]};
+    // keys: channel d, tokens [part * TP, part * TP + TP)
+    const int P = RB_THREADS / D, TP = KG / P;
+    const int d = tid / P, part = tid % P, t0 = part * TP;
+    float lo = INFINITY, hi = -INFINITY;
+    for (int t = 0; t < TP; ++t) {
+        lo = fminf(lo, xk[t0 + t][d]);
+        hi = fmaxf(hi, xk[t0 + t][d]);
+    }
+    for (int m = 1; m < P; m <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, m));
+        hi = fmaxf(hi, __shfl_xor(hi, m));
+    }
+    const QuantGroup qp = quant_params(lo, hi, MA_BF16);
+    uint32_t w[2] = {0, 0};
+    for (int t = 0; t < TP; ++t) w[t >> 3] |= quant_code(xk[t0 + t][d], qp, MA_BF16) << ((t & 7) * 4);
+    uint8_t *krow = n.kq + (int64_t)g * n.kq_g + d * n.kq_d + t0 / 2;
+    if (TP == 16) *(uint2 *)krow = uint2{w[0], w[1]};
+    else *(uint32_t *)krow = w[0];
+    if (part == 0) {
         const _Float16 s16 = (_Float16)qp.step, z16 = (_Float16)qp.lo;
         n.ks[(int64_t)g * n.ks_g + d] = *(const uint16_t *)&s16;
         n.kz[(int64_t)g * n.ks_g + d] = *(const uint16_t *)&z16;
-    }
-    // values: one token's channel group
-    for (int u = tid; u < KG * ncg; u += RB_THREADS) {
-        const int t = u / ncg, c = u % ncg;
-        float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < VG; ++i) {
-            lo = fminf(lo, xv[t][c * VG + i]);
-            hi = fmaxf(hi, xv[t][c * VG + i]);
-        }
-        const QuantGroup qp = quant_params(lo, hi, MA_BF16);
-        uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < VG; ++i) w[i >> 3] |= quant_code(xv[t][c * VG + i], qp, MA_BF16) << ((i & 7) * 4);
-        const int64_t tok = (int64_t)g * KG + t;
-        *(uint4 *)(n.vq + tok * n.vq_n + c * n.vq_c) = uint4{w[0], w[1], w[2], w[3]};
-        const _Float16 s16 = (_Float16)qp.step, z16 = (_Float16)qp.lo;
-        n.vs[tok * n.vs_n + c] = *(const uint16_t *)&s16;
-        n.vz[tok * n.vs_n + c] = *(const uint16_t *)&z16;
     }
 }
 

@@ -261,12 +261,14 @@ class EvictionState:
         return rank, window
 
     def survivors(self, cfg: EvictionConfig, capacity: int, value_spread: torch.Tensor | None = None,
-                  score: torch.Tensor | None = None) -> torch.Tensor:
+                  score: torch.Tensor | None = None, check: bool = True) -> torch.Tensor:
         """Live-axis indices of the `capacity` entries to keep in every lane, [L, B, Hkv, C],
-        in position order: the policy's contest solved by ma_keep_select."""
+        in position order: the policy's contest solved by ma_keep_select.  check=False skips
+        the read-back of the positions' order check (append admits increasing positions
+        after the live ones, so the state keeps them ascending)."""
         rank, window = self._contest(cfg, capacity, value_spread, score)
         return keep_select(self._in_use("pos"), rank.contiguous(), capacity, window, sink_tokens=cfg.sink_tokens,
-                           pin=self._pin_rows())
+                           pin=self._pin_rows(), check=check)
 
     def _pin_rows(self):
         """The pinned position range (lo, hi): lo an int or a per-sequence [B] tensor."""

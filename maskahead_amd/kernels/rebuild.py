@@ -82,13 +82,15 @@ def rebuild_plan(phys: torch.Tensor, pos: torch.Tensor, live: int, *, quantized_
 
 def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Tensor, encode: torch.Tensor,
                    groups_after: torch.Tensor, stage: torch.Tensor, remap: torch.Tensor,
-                   phys: torch.Tensor | None = None, live: int = 0) -> None:
+                   phys: torch.Tensor | None = None, live: int = 0, check: bool = True) -> torch.Tensor | None:
     """One launch of ``ma_rebuild_packed``: old / new are Prefix descriptors of the storage
     with layers folded into the batch axis (B = layers x batch); lists [lanes..., n]
     int64; remap int64 [lanes..., old length] written whole; phys (optional) int32
     [lanes..., capacity] rewritten in place for its first ``live`` entries.  Raises
     RuntimeError for a list entry outside the old storage (as the reference's gathers
-    do) and AssertionError when a live entry maps to no new slot (session.py:354-355)."""
+    do) and AssertionError when a live entry maps to no new slot (session.py:354-355).
+    check=False skips that read-back (a host synchronisation) and returns the per-lane
+    status tensor instead, for raise_rebuild_status at a later synchronisation point."""
     lists = [_lanes2d(t, n) for t, n in ((groups_before, "groups_before"), (encode, "encode"),
                                          (groups_after, "groups_after"), (stage, "stage"))]
     lanes = B * H
@@ -114,7 +116,15 @@ def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Ten
            ga.data_ptr(), _stride(ga), ga.shape[1], stg.data_ptr(), _stride(stg), stg.shape[1],
            r2.data_ptr(), r2.stride(0), ph_ptr, ph_stride, int(live if ph_ptr else 0), status.data_ptr(),
            N.stream_of(remap))
-    s = int(status.cpu().max()) if lanes else 0   # one small copy, no reduction kernel
+    if not check:
+        return status
+    raise_rebuild_status(status)
+    return None
+
+
+def raise_rebuild_status(status: torch.Tensor) -> None:
+    """The errors of a rebuild from its per-lane status (one small copy to the host)."""
+    s = int(status.cpu().max()) if status.numel() else 0   # no reduction kernel
     if s & 1:
         raise RuntimeError("rebuild: an index list names a slot or key group outside the cache")
     if s & 2:

@@ -29,7 +29,7 @@ def value_score(a: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
 
 
 def evict_to(cache, state, keep: torch.Tensor, cfg, *, next_position: int, phys_compact: bool = True,
-             state_done: bool = False) -> None:
+             state_done: bool = False, check: bool = True) -> None:
     """Keep live entries keep [L, B, Hkv, C]; then bring the physical cache in line
     (``BitSieveSession._evict_to``, session.py:270-361).
 
@@ -42,7 +42,9 @@ def evict_to(cache, state, keep: torch.Tensor, cfg, *, next_position: int, phys_
     compacted exactly.  ``next_position``: the first position not admitted yet (the
     session's _next_position).  The plan runs in ma_rebuild_plan, the data movement and
     the state's new slots in one ma_rebuild_packed launch; two host synchronisations
-    (the plan's counts and the rebuild's status), as in the reference."""
+    (the plan's counts and the rebuild's status), as in the reference.  check=False keeps
+    only the first: the rebuild's status is read at the next rebuild (or
+    cache.check_rebuild())."""
     import math
 
     from ..kernels.rebuild import rebuild_plan
@@ -83,7 +85,7 @@ def evict_to(cache, state, keep: torch.Tensor, cfg, *, next_position: int, phys_
         groups_after = torch.arange(ng - tail_groups, ng, device=dev).expand(L, B, H, tail_groups)
     else:
         groups_after = empty
-    cache._rebuild(groups_before, enc_slots, groups_after, stage_slots, phys=state.phys, live=live)
+    cache._rebuild(groups_before, enc_slots, groups_after, stage_slots, phys=state.phys, live=live, check=check)
 
 
 def live_slot_masks(cache, state) -> dict:
@@ -136,13 +138,17 @@ def lookahead_scores(cache, state, a1: dict, a_probe: dict | None = None, *, use
 
 
 def lookahead_evict(cache, state, cfg, capacity: int, a1: dict, a_probe: dict | None = None, *,
-                    next_position: int, phys_compact: bool = True):
+                    next_position: int, phys_compact: bool = True, check: bool = True):
     """Evict to `capacity` with the lookahead score (session.py:1985-2034): the survivors
     of the eviction state (ma_keep_select) under that score, then evict_to.  Returns the
-    keep set, or None when the live set already fits."""
+    keep set, or None when the live set already fits.  check=False (a decode loop's hot
+    path) skips the two error read-backs that cost a host synchronisation each -- the keep
+    set's order check, whose positions the state keeps ascending by construction, and the
+    rebuild's status, read at the next rebuild -- leaving the plan's count read-back as
+    the eviction's only synchronisation."""
     if state.live <= capacity:
         return None
     score = lookahead_scores(cache, state, a1, a_probe, use_value=cfg.lookahead_score != "mass")
-    keep = state.survivors(cfg, capacity, None, score)
-    evict_to(cache, state, keep, cfg, next_position=next_position, phys_compact=phys_compact)
+    keep = state.survivors(cfg, capacity, None, score, check=check)
+    evict_to(cache, state, keep, cfg, next_position=next_position, phys_compact=phys_compact, check=check)
     return keep

@@ -133,7 +133,9 @@ def test_lookahead_probe_evict_then_masked_attention(gpu):
         assert torch.equal(score2[layer].cpu(), OA.value_score_bf16(a, vd2[layer].gather(2, gi)))
     C2 = 768
     pos1 = st.pos[..., :live].cpu().to(torch.int64)
-    keep2 = lookahead_evict(cache, st, cfg, C2, a1b, fp.probe_mass, next_position=n)
+    # the decode loop's hot path: no order-check or rebuild-status read-back
+    keep2 = lookahead_evict(cache, st, cfg, C2, a1b, fp.probe_mass, next_position=n, check=False)
     torch.cuda.synchronize()
     assert torch.equal(keep2.cpu(), OS.keep_select(pos1, score2.cpu(), C2, W))
     assert st.live == C2
+    cache.check_rebuild()

@@ -174,6 +174,17 @@ def test_rebuild_direct_lists_and_errors(gpu):
     with pytest.raises(RuntimeError):
         cache.rebuild(gb.to(gpu), torch.tensor([[5, 144, -1], [1, 2, 3]]).view(1, 1, 2, 3).to(gpu), ga.to(gpu),
                       stg.to(gpu))
+    # check=False: the same error, raised by the next check instead of the call
+    cache = _cache_from(store, lens, gpu)
+    cache._rebuild(gb.to(gpu), torch.tensor([[5, 144, -1], [1, 2, 3]]).view(1, 1, 2, 3).to(gpu), ga.to(gpu),
+                   stg.to(gpu), check=False)
+    with pytest.raises(RuntimeError):
+        cache.check_rebuild()
+    cache.check_rebuild()                         # raised once, then nothing pending
+    cache = _cache_from(store, lens, gpu)
+    cache._rebuild(gb.to(gpu), enc.to(gpu), ga.to(gpu), stg.to(gpu), check=False)
+    cache.check_rebuild()
+    _check_cache(cache, want, want_lens)
 
 
 def test_evict_to_bf16_cache_with_tail(gpu):
