@@ -657,7 +657,10 @@ __global__ void __launch_bounds__(128) splitk_combine_kernel(FwdArgs a, ma_tenso
     __shared__ float red[CMB_SL][D];
     __shared__ float lred[CMB_SL];
     __shared__ float smax[128 / 64];
-    const int row = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    // workgroup id -> (row, lane) lane-fastest, as pass 1 numbers its workgroups, so a
+    // lane's rows are merged on the XCDs whose L2 took that lane's partials
+    const int BH = gridDim.x / a.R;
+    const int row = blockIdx.x / BH, bh = blockIdx.x % BH, b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x;
     const int R = a.R, nsplit = a.nsplit;
     const int64_t base = (int64_t)bh * (nsplit + 1) * R + row;
@@ -928,7 +931,7 @@ int launch_merge(const Plan &pl, ma_tensor4 out, float *mp, float *lp, void *op,
         return MA_EINVAL;
     }
     const FwdArgs &fa = pl.fa;
-    const dim3 cgrid(fa.R, pl.B * fa.H);
+    const dim3 cgrid(fa.R * pl.B * fa.H);
     if (pl.D == 128)
         hipLaunchKernelGGL(splitk_combine_kernel<128>, cgrid, dim3(128), 0, st, fa, out, mp, lp, op);
     else
