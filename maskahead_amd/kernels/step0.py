@@ -32,6 +32,11 @@ class Step0Buffers:
 
     def __init__(self):
         self._store: dict = {}
+        # the last call's checked arguments and ctypes argument list (step0_select reuses
+        # them while the prefix object, the shapes, the selection rows, the output views,
+        # the workspace owner and the stream are the same: only the three operands' pointers
+        # change from call to call)
+        self._plan: tuple | None = None
 
     def take(self, name: str, numel: int, dtype: torch.dtype, device: torch.device, shape: tuple) -> torch.Tensor:
         t = self._store.get(name)
@@ -51,6 +56,21 @@ def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, curren
     selected entries are gathered into (the layer's compact buffer).  workspace: where the
     scratch workspace lives (default bufs); layers run one after another on a stream can
     share one."""
+    stream = N.stream_of(query)
+    rows_key = rows if isinstance(rows, torch.Tensor) else tuple(rows)
+    views = tuple(None if x is None else (x.data_ptr(), x.shape, x.stride(), x.dtype) for x in (out_key, out_value))
+    key = (query.shape, query.stride(), query.dtype, current_key.shape, current_key.stride(), current_value.stride(),
+           current_key.dtype, int(k), bool(value), scaling, views, stream)
+    plan = bufs._plan
+    if (plan is not None and plan[0] is prefix and plan[1] is workspace and plan[2] == key
+            and (plan[3] is rows_key if isinstance(rows_key, torch.Tensor) else plan[3] == rows_key)):
+        args, result = plan[4], plan[5]
+        tc = current_key.shape[2]
+        args[0] = N.t4(query)
+        args[7] = N.t4(current_key if tc else None)
+        args[8] = N.t4(current_value if tc else None)
+        N.check(N.load().ma_step0(*args), "ma_step0")
+        return result
     if query.ndim != 4 or current_key.ndim != 4:
         raise ValueError("query and current_key must be [B, H, T, D]")
     N.require_gpu(query, "query")
@@ -92,14 +112,18 @@ def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, curren
     if ws_bytes <= 0:
         raise N.KernelUnavailableError(f"ma_step0: no workspace size for n={n}")
     ws = (workspace or bufs).take("ws", ws_bytes, torch.uint8, dev, (ws_bytes,))
-    stream = N.stream_of(query)
     st = _state(dev, N.size_query("ma_topk_state_bytes", b * hkv), stream)
     scale = float(scaling) if scaling is not None else d ** -0.5
     tc = current_key.shape[2]
-    rc = N.load().ma_step0(
-        N.t4(query), b, hq, t, d, nat, hkv, N.t4(current_key if tc else None), N.t4(current_value if tc else None),
-        tc, scale, N.t4(out), mp.data_ptr(), lp.data_ptr(), op.data_ptr(), N.ptr(q_rows), t2, 1 if value else 0,
-        2 if value else 1, vround, mass.data_ptr(), N.ptr(score), k, idx.data_ptr(), N.t4(out_key),
-        N.t4(out_value), st.data_ptr(), st.numel(), ws.data_ptr(), ws_bytes, stream)
-    N.check(rc, "ma_step0")
-    return out, (mp, lp, op, used), mass, score, idx
+    args = [N.t4(query), b, hq, t, d, nat, hkv, N.t4(current_key if tc else None),
+            N.t4(current_value if tc else None), tc, scale, N.t4(out), mp.data_ptr(), lp.data_ptr(), op.data_ptr(),
+            N.ptr(q_rows), t2, 1 if value else 0, 2 if value else 1, vround, mass.data_ptr(), N.ptr(score), k,
+            idx.data_ptr(), N.t4(out_key), N.t4(out_value), st.data_ptr(), st.numel(), ws.data_ptr(), ws_bytes,
+            stream]
+    N.check(N.load().ma_step0(*args), "ma_step0")
+    result = (out, (mp, lp, op, used), mass, score, idx)
+    # the plan keeps every tensor its pointers name alive: q_rows (a cached device table, or
+    # None), the select state and the workspace (which another layer sharing the owner may
+    # have replaced by a larger one since)
+    bufs._plan = (prefix, workspace, key, rows_key, args, result, q_rows, st, ws)
+    return result

@@ -78,6 +78,29 @@ def test_step0_fused_reuses_buffers(gpu):
     _check(gpu, bufs, ws, q3, p3, kc3, vc3, list(range(8)), 128, value=True)
 
 
+def test_step0_fused_repeat_calls(gpu):
+    """A layer's repeated step 0 with new operands (same shapes, the same prefix object,
+    rows and output views): the call reuses its checked arguments and gives the stages'
+    results every time; a change of read budget re-plans."""
+    bufs, ws = Step0Buffers(), Step0Buffers()
+    _, p, _, _ = _case(gpu, 4096, 40, dead=True, seed=11)
+    b, hkv, k = 1, 4, 512
+    ck = torch.empty((b, hkv, 1024, 128), dtype=torch.bfloat16, device=gpu)
+    cv = torch.empty_like(ck)
+    plans = []
+    for i, kk in enumerate((k, k, k, 300)):
+        q, _, kc, vc = _case(gpu, 4096, 40, dead=True, seed=20 + i)
+        want = _reference(q, p, kc, vc, list(range(32)), kk, True)
+        out, stats, mass, score, idx = step0_select(bufs, q, p, kc, vc, list(range(32)), kk, value=True,
+                                                    out_key=ck[:, :, :kk], out_value=cv[:, :, :kk], workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want[0]) and torch.equal(mass, want[2]) and torch.equal(score, want[3])
+        assert torch.equal(idx, want[4])
+        assert torch.equal(ck[:, :, :kk], want[5]) and torch.equal(cv[:, :, :kk], want[6])
+        plans.append(bufs._plan[4])
+    assert plans[0] is plans[1] is plans[2] and plans[3] is not plans[2]
+
+
 def test_step0_fused_errors(gpu):
     bufs = Step0Buffers()
     q, p, kc, vc = _case(gpu, 1024, 0, seed=8)
