@@ -368,6 +368,18 @@ class PackedKVCache:
             key_token_group=self.quant.key_token_group, value_channel_group=self.quant.value_channel_group,
             head_dim=self.head_dim, key_mode=self.quant.key_mode, k_chan=None, **cut)
 
+    def all_layers_view(self) -> LayerCacheView:
+        """Every layer's stored prefix as one view with the layers folded into the batch axis
+        ([L * B, H, rows, ...] planes, rows in use), for kernels that treat every (layer,
+        batch, KV head) lane alike."""
+        cut = {name: None if getattr(self, name) is None
+               else getattr(self, name)[:, :, :, :self._rows_in_use(_UNITS[name])].flatten(0, 1) for name in _UNITS}
+        return LayerCacheView(
+            k_bits=self.quant.k_bits, v_bits=self.quant.v_bits, length=self.length,
+            quantized_length=self.quantized_length, residual_length=self.residual_length,
+            key_token_group=self.quant.key_token_group, value_channel_group=self.quant.value_channel_group,
+            head_dim=self.head_dim, key_mode=self.quant.key_mode, k_chan=None, **cut)
+
     def dequantize_layer(self, layer_idx: int, *, dtype: torch.dtype | None = None):
         """One layer's whole stored prefix as [B, H, length, D] K and V (ma_dequant_prefix)."""
         from .kernels.splitk import Prefix, dequantize_prefix

@@ -24,6 +24,7 @@ from dataclasses import dataclass, field
 
 import torch
 
+from .. import _native as N
 from .._native import KernelUnavailableError
 from ..kernels.splitk import Prefix, prefix_scores, splitk_attention
 from ..kernels.step0 import Step0Buffers, step0_select
@@ -282,15 +283,31 @@ class FastLayerPath:
         if k + ncur > state.key.shape[2]:
             raise RuntimeError("compact cache buffer capacity exceeded")
         cd = self.compute_dtype
-        key = (k, state.key.data_ptr(), state.value.data_ptr(), state.key.stride(), state.value.stride())
+        q, kc, vc = query.to(cd), current_key.to(cd), current_value.to(cd)
+        stream = N.stream_of(q)
+        key = (k, state.key.data_ptr(), state.value.data_ptr(), state.key.stride(), state.value.stride(),
+               q.shape, q.stride(), kc.shape, kc.stride(), vc.stride(), stream)
         hit = self._compact_prefix.get(layer_idx)
         if hit is not None and hit[0] == key:
-            pre = hit[1]   # the same compact buffer, length and strides: the same descriptor
-        else:
-            pre = Prefix.dense(state.key[:, :, :k, :], state.value[:, :, :k, :])
-            self._compact_prefix[layer_idx] = (key, pre)
-        out, _ = splitk_attention(query.to(cd), pre, current_key.to(cd), current_value.to(cd),
-                                  scaling=self.head_dim ** -0.5)
+            # the same compact buffer, shapes and stream: the call checked and packed before,
+            # with this call's operands and a fresh output
+            args = hit[2]
+            out = torch.empty_like(q)
+            tc = kc.shape[2]
+            args[0], args[7], args[8], args[14] = N.t4(q), N.t4(kc if tc else None), N.t4(vc if tc else None), N.t4(out)
+            N.check(N.load().ma_splitk_attention(*args), "ma_splitk_attention")
+            return out.to(query.dtype)
+        pre = Prefix.dense(state.key[:, :, :k, :], state.value[:, :, :k, :])
+        out, _ = splitk_attention(q, pre, kc, vc, scaling=self.head_dim ** -0.5)
+        # the arguments of that call, for the next sub-steps of this layer (splitk_attention's
+        # own; the workspace is kept with them)
+        b, hq, t, d = q.shape
+        hkv, tc = kc.shape[1], kc.shape[2]
+        ws_bytes = N.size_query("ma_splitk_workspace_bytes", b, hkv, hq, t, d, pre.nq, pre.nf, 0)
+        ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+        args = [N.t4(q), b, hq, t, d, pre.native(), hkv, N.t4(kc if tc else None), N.t4(vc if tc else None), tc, 0, 0,
+                0, float(self.head_dim ** -0.5), N.t4(out), None, None, None, 0, ws.data_ptr(), ws_bytes, stream]
+        self._compact_prefix[layer_idx] = (key, pre, args, ws)
         return out.to(query.dtype)
 
     def question_probe(self, layer_idx, query, current_key, current_value, *, q_pos0: int, live_slots=None):

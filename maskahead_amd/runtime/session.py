@@ -120,20 +120,22 @@ def lookahead_scores(cache, state, a1: dict, a_probe: dict | None = None, *, use
     from ..kernels.keep import value_score_slots
     from ..kernels.splitk import Prefix
 
-    L = state.num_layers
-    score = torch.empty((L, cache.batch_size, cache.num_kv_heads, state.live), dtype=torch.float32,
-                        device=cache.device)
+    L, B, H, live = state.num_layers, cache.batch_size, cache.num_kv_heads, state.live
+    a_all = torch.empty((L, B, H, live), dtype=torch.float32, device=cache.device)
     for layer in range(L):
         a = a1[layer]
         if a_probe is not None and layer in a_probe:
             a = a + a_probe[layer]
-        if use_value:
-            # value_score(a, live_values(cache, state, layer)), from the cache's codes
-            # directly (the same bits, no gathered [B, Hkv, live, D] rows)
-            value_score_slots(a.contiguous(), Prefix.from_view(cache.layer_view(layer)),
-                              state.phys[layer, ..., :state.live], dtype=cache.compute_dtype, out=score[layer])
-        else:
-            score[layer] = a
+        a_all[layer] = a
+    if not use_value:
+        return a_all
+    # value_score(a, live_values(cache, state, layer)) of every layer in one call, the layers
+    # folded into the batch axis, from the cache's codes directly (the same bits, no gathered
+    # [B, Hkv, live, D] rows)
+    score = torch.empty_like(a_all)
+    value_score_slots(a_all.view(L * B, H, live), Prefix.from_view(cache.all_layers_view()),
+                      state.phys[..., :live].reshape(L * B, H, live), dtype=cache.compute_dtype,
+                      out=score.view(L * B, H, live))
     return score
 
 
