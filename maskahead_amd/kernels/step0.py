@@ -62,8 +62,11 @@ def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, curren
     key = (query.shape, query.stride(), query.dtype, current_key.shape, current_key.stride(), current_value.stride(),
            current_key.dtype, int(k), bool(value), scaling, views, stream)
     plan = bufs._plan
+    # (prefix.native() returns the same descriptor object while the prefix's tensors and
+    # mask are the ones it was built from)
     if (plan is not None and plan[0] is prefix and plan[1] is workspace and plan[2] == key
-            and (plan[3] is rows_key if isinstance(rows_key, torch.Tensor) else plan[3] == rows_key)):
+            and (plan[3] is rows_key if isinstance(rows_key, torch.Tensor) else plan[3] == rows_key)
+            and plan[4][5] is prefix.native()):
         args, result = plan[4], plan[5]
         tc = current_key.shape[2]
         args[0] = N.t4(query)
