@@ -100,3 +100,49 @@ def test_fast_path_supported_reasons():
     assert fast_path_supported(_cfg(quant=QuantizationConfig(k_bits=2, v_bits=2)), 128)[1] == "bits"
     assert fast_path_supported(_cfg(quant=QuantizationConfig(key_token_group=16)), 128)[1] == "group sizes"
     assert fast_path_supported(_cfg(quant=QuantizationConfig(k_bits=16, v_bits=16)), 64) == (True, "head_dim")
+
+
+def _bind_target(cfg, head_dim=128):
+    """A session-shaped object with the members bind_session reads at bind time."""
+    class Session:
+        def _fast_step0(self, *a):
+            return "reference"
+
+        def _compact_attention(self, *a):
+            return "reference"
+
+    s = Session()
+    cfg.selector.sort_indices, cfg.selector.dense_prefix_layers = True, 0
+    cfg.generation = SimpleNamespace(block_size=32)
+    s.config, s.head_dim, s.compute_dtype, s._states, s._eviction = cfg, head_dim, torch.bfloat16, {}, None
+    s.cache = SimpleNamespace(device=torch.device("cuda"))
+    return s
+
+
+def test_bind_session_host():
+    """bind_session refuses a configuration the HIP path does not serve and leaves the
+    session as it was; otherwise it replaces the fast-path methods on that instance only,
+    the class and the session's compact states left shared."""
+    from maskahead_amd.runtime.bind import bind_session, bind_value_score
+
+    s = _bind_target(_cfg(selector__mode="uniform"))
+    with pytest.raises(KernelUnavailableError, match="selector score/domain/mode"):
+        bind_session(s)
+    assert s._fast_step0() == "reference" and "_fast_step0" not in vars(s)
+    s = _bind_target(_cfg(), head_dim=96)
+    with pytest.raises(KernelUnavailableError, match="head_dim"):
+        bind_session(s)
+
+    s = _bind_target(_cfg())
+    fp = bind_session(s)
+    for name in ("_fast_step0", "_compact_attention", "_fast_attend", "_current_only", "_prefix", "_live_values"):
+        assert name in vars(s), name
+    assert "_evict_to" not in vars(s)                 # another cache type keeps its own eviction
+    assert fp.states is s._states and fp.block_size == 32 and fp.value_aware
+    assert type(s)()._fast_step0() == "reference"
+
+    mod = SimpleNamespace(value_score=lambda a, v: None)
+    old = bind_value_score(mod)
+    from maskahead_amd.runtime.session import value_score
+
+    assert mod.value_score is value_score and old is not value_score
