@@ -80,8 +80,12 @@ const char *ma_last_error(void);
 int ma_version(void);
 
 /* dequantize_prefix (splitk.py:465-480; codec reference.py:48-55, 168-179, 259-268):
- * the whole prefix as [B,H,n,D] K and V in out dtype (bf16 or f32), n = nq + nf.
- * Bit-exact: x = f32(code)*f32(scale) + f32(zero), rounded to nearest even. */
+ * the whole prefix as [B,H,n,D] K and V in out dtype (bf16, f16 or f32), n = nq + nf.
+ * Bit-exact: x = f32(code)*f32(scale) + f32(zero), rounded to nearest even.  The split-K
+ * and score entry points read a packed prefix with each value rounded to bf16 once, as
+ * the reference's kernels do; the reference's host dispatch first unpacks a long packed
+ * prefix to the query dtype (splitk.py:513-516), which for f16 queries rounds through
+ * f16 as well: that caller passes this call's f16 copy as a 16-bit prefix instead. */
 int ma_dequant_prefix(const ma_prefix *p, int B, int H, int D, ma_tensor4 k_out, ma_tensor4 v_out,
                       void *stream);
 

@@ -192,11 +192,19 @@ def splitk_attention(query, prefix: Prefix, current_key, current_value, *, scali
     r = g * t
     prefix.check_mask(b, hkv)
     # the reference unpacks such a prefix to query.dtype and reads that copy from here on
-    # (splitk.py:513-516); the statistics carry a copy that says so
+    # (splitk.py:513-516).  For bf16 queries the copy holds what the kernels read anyway
+    # (each dequantized value rounded to bf16 once): the statistics carry a descriptor
+    # that marks the value distance to round V to bf16 too.  For f16 queries the copy's
+    # values are rounded f32 -> f16 and every dot rounds them again, f16 -> bf16: the
+    # copy is made (ma_dequant_prefix) and read from here on, as the reference does.
     used = prefix
     nat = prefix.native()   # built before the copy below, which then shares it
     if prefix.nq and (r > dequant_rows or prefix.n > packed_direct_max) and query.dtype != torch.float32:
-        used = prefix.with_vround(N.dtype_code(query.dtype))
+        if query.dtype == torch.float16:
+            used = Prefix.dense(*dequantize_prefix(prefix, b, hkv, d, dtype=torch.float16), mask=prefix.mask)
+            nat = used.native()
+        else:
+            used = prefix.with_vround(N.dtype_code(query.dtype))
     dev = query.device
     scale = float(scaling) if scaling is not None else d ** -0.5
     out = torch.empty_like(query)

@@ -13,15 +13,35 @@ import torch
 
 from .. import _native as N
 from .select import _state
-from .splitk import Prefix
+from .splitk import Prefix, splitk_attention
+
+
+def _unpacked(prefix: Prefix, r: int, query: torch.Tensor) -> bool:
+    """Whether the reference reads this packed prefix through a copy unpacked to the
+    query dtype (splitk.py:513-516), as splitk_attention does."""
+    return bool(prefix.nq) and (r > 256 or prefix.n > 256) and query.dtype != torch.float32
 
 
 def _vround(prefix: Prefix, r: int, query: torch.Tensor) -> int:
-    """The dtype the reference reads a long packed prefix through (splitk.py:513-516), as
-    splitk_attention records it in its statistics."""
-    if prefix.nq and (r > 256 or prefix.n > 256) and query.dtype != torch.float32:
-        return N.dtype_code(query.dtype)
-    return 0
+    """The dtype of that copy, as splitk_attention records it in its statistics (bf16
+    queries; an f16 copy is made and read instead, see _staged)."""
+    return N.dtype_code(query.dtype) if _unpacked(prefix, r, query) else 0
+
+
+def _staged(query, prefix, current_key, current_value, rows, k, value, scale, out_key, out_value):
+    """Step 0 as its stages, for f16 queries over an unpacked packed prefix: splitk_attention
+    makes the f16 copy the reference reads (K and V rounded f32 -> f16, then f16 -> bf16 at
+    every dot) and the scores, the read set and the gather read that copy."""
+    from .ops import gather_packed_kv
+    from .select import prefix_scores_topk
+
+    out, stats = splitk_attention(query, prefix, current_key, current_value, scaling=scale, want_prefix=True)
+    mass, score, idx = prefix_scores_topk(query, prefix, stats, rows, k, value=value,
+                                          rank="score" if value else "mass", scaling=scale)
+    if out_key is not None or out_value is not None:
+        gather_packed_kv(stats[3], idx, dtype=(out_key if out_key is not None else out_value).dtype,
+                         out_key=out_key, out_value=out_value)
+    return out, stats, mass, score, idx
 
 
 class Step0Buffers:
@@ -100,6 +120,9 @@ def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, curren
         t2 = len(host)
     if t2 == 0:
         raise ValueError("q_rows cannot be empty")
+    if query.dtype == torch.float16 and _unpacked(prefix, r, query):
+        return _staged(query, prefix, current_key, current_value, rows, k, value,
+                       float(scaling) if scaling is not None else d ** -0.5, out_key, out_value)
     dev = query.device
     nat = prefix.native()
     vround = _vround(prefix, r, query)

@@ -16,7 +16,9 @@ from maskahead_amd import _native as N
 from maskahead_amd.cache import PackedKVCache
 from maskahead_amd.config import QuantizationConfig
 from maskahead_amd.kernels.ops import _selected_queries, dense_packed_attention, selector_topk
+from maskahead_amd.kernels.select import prefix_scores_topk
 from maskahead_amd.kernels.splitk import Prefix, prefix_scores, splitk_attention
+from maskahead_amd.kernels.step0 import Step0Buffers, step0_select
 from maskahead_amd.runtime.fastpath import BlockContext, FastLayerPath
 from maskahead_amd.workloads import layer_inputs
 from oracle import attention as OA
@@ -100,25 +102,44 @@ def test_value_centre_against_oracle(gpu):
     assert rel_err(centre, want) < 1e-6
 
 
-def test_scores_round_packed_values_to_query_dtype(gpu):
+def test_f16_queries_read_an_f16_copy_of_a_packed_prefix(gpu):
     """A packed prefix longer than packed_direct_max is read by the reference through a copy
-    unpacked to the query dtype (splitk.py:513-516): with f16 queries the value distance
-    sees f16-rounded values.  The caller's Prefix is left as it was."""
+    unpacked to the query dtype (splitk.py:513-516): with f16 queries K and V are rounded
+    f32 -> f16 into that copy and f16 -> bf16 at every dot, and the value distance sees the
+    f16 values.  The copy is bit-identical to the oracle's dequantization rounded to f16;
+    attention, statistics, scores and the step-0 call follow it.  The caller's Prefix is
+    left as it was."""
     q, k, v, kc, vc = layer_inputs(b=1, hq=28, hkv=4, d=128, n=1024, t=32, seed=55)
     store, nq = packed_cpu(k.to(torch.bfloat16), v.to(torch.bfloat16))
     pre = gpu_prefix(store, nq, gpu)
     qh, kch, vch = q.to(torch.float16), kc.to(torch.float16), vc.to(torch.float16)
     out, stats = splitk_attention(qh.to(gpu), pre, kch.to(gpu), vch.to(gpu), want_prefix=True)
-    assert pre.vround == 0 and stats[3].vround == N.MA_F16
-    mass, score = prefix_scores(qh.to(gpu), pre, stats, torch.arange(32, dtype=torch.int32), value=True)
+    used = stats[3]
+    assert pre.vround == 0 and pre.nq == nq and used.nq == 0 and used.kf.dtype == torch.float16
     kd, vd = dequant_cpu(store, nq)
+    kd16, vd16 = kd.to(torch.float16), vd.to(torch.float16)
+    assert torch.equal(used.kf.cpu(), kd16) and torch.equal(used.vf.cpu(), vd16)
+    wout, wmp, wlp, wop = OA.splitk_attention(qh, kd16, vd16, kch, vch)
+    assert_attention_close(out, wout)
+    assert rel_err(stats[0], wmp) < 1e-5 and rel_err(stats[1], wlp) < 1e-4
+    # the bar has teeth: rounding K and V to bf16 once gives statistics outside it
+    _, smp, slp, _ = OA.splitk_attention(qh, kd, vd, kch, vch)
+    assert rel_err(smp, wmp) > 1e-4 or rel_err(slp, wlp) > 1e-3
+    mass, score = prefix_scores(qh.to(gpu), pre, stats, torch.arange(32, dtype=torch.int32), value=True)
     mp, lp, op = (x.cpu() for x in stats[:3])
-    wmass, wscore = OA.prefix_scores(qh, kd, vd.to(torch.float16).float(), mp, lp, op, range(32), value_aware=True)
+    wmass, wscore = OA.prefix_scores(qh, kd16, vd16.float(), mp, lp, op, range(32), value_aware=True)
     assert rel_err(mass, wmass) < 1e-4
     assert rel_err(score, wscore) < 1e-4
-    # f32 values differ from the f16-rounded ones somewhere: the rounding is not a no-op
-    _, wscore32 = OA.prefix_scores(qh, kd, vd, mp, lp, op, range(32), value_aware=True)
-    assert not torch.equal(wscore32, wscore)
+    # the one-call step 0 gives the same (it runs the stages for this case)
+    ck = torch.empty((1, 4, 256, 128), dtype=torch.float16, device=gpu)
+    cv = torch.empty_like(ck)
+    out2, stats2, mass2, score2, idx2 = step0_select(Step0Buffers(), qh.to(gpu), pre, kch.to(gpu), vch.to(gpu),
+                                                     list(range(32)), 256, value=True, out_key=ck, out_value=cv)
+    _, _, widx = prefix_scores_topk(qh.to(gpu), pre, stats, list(range(32)), 256, value=True)
+    assert torch.equal(out2, out) and torch.equal(mass2, mass) and torch.equal(score2, score)
+    assert torch.equal(idx2, widx)
+    gi = widx.cpu().unsqueeze(-1).expand(-1, -1, -1, 128)
+    assert torch.equal(ck.cpu(), kd16.gather(2, gi)) and torch.equal(cv.cpu(), vd16.gather(2, gi))
 
 
 def test_mask_of_the_wrong_shape_is_rejected(gpu):
