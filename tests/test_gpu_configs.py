@@ -8,9 +8,12 @@
   each sequence one block -- step 0 of every layer, the lookahead eviction that follows it
   (keep set + packed lazy rebuild, session.py:1985-2034, 270-361), 3 sub-steps, and the
   block's finalize (its KV appended).  The oracle checks the shortest and the longest
-  sequence on one dense and one sparse layer (KV head 0), every keep set (bit-exact) and
-  the rebuilt cache of the shortest sequence (bit-exact); every other layer and sequence
-  gets the invariants (finite outputs; read sets ascending, unique, live, of the budget)."""
+  sequence on one dense and one sparse layer (all KV heads), every keep set (bit-exact) and
+  the rebuilt cache of the shortest sequence (bit-exact); every sparse layer of every
+  sequence, all KV heads, has its read set equal to the oracle's top-k of the scores the
+  same passes give (bit-exact) and its step-0 mass equal to theirs; every other layer and
+  sequence gets the invariants (finite outputs; read sets ascending, unique, live, of the
+  budget)."""
 
 from __future__ import annotations
 
@@ -147,25 +150,30 @@ def test_config4_ragged_block_step(gpu):
             assert torch.isfinite(out.float()).all()
             if layer >= dense:
                 _check_read_set_invariants(fp.states[layer].indices, n, read_k)
+                # every sparse layer, every KV head: the read set is the oracle's top-k of
+                # the scores the same passes give, and step 0 kept their mass
+                pre = fp.prefix(layer)
+                _, sts = splitk_attention(q, pre, kc, vc, want_prefix=True)
+                gmass, gscore = prefix_scores(q, pre, sts, torch.arange(t, dtype=torch.int32), value=True)
+                assert torch.equal(fp.last_mass[layer], gmass)
+                assert torch.equal(fp.states[layer].indices.cpu(), OS.topk_ascending(gscore.cpu(), read_k)), \
+                    (i, layer)
             else:
                 assert layer not in fp.states
             if layer in checked:
                 kd, vd = views[layer]
                 qc, kcc, vcc = q.cpu(), kc.cpu(), vc.cpu()
-                wout, wmp, wlp, wop = OA.splitk_attention(qc[:, :7], kd[:, :1], vd[:, :1], kcc[:, :1], vcc[:, :1])
-                assert_attention_close(out[:, :7], wout)
+                wout, wmp, wlp, wop = OA.splitk_attention(qc, kd, vd, kcc, vcc)
+                assert_attention_close(out, wout)
                 if layer >= dense:
-                    pre = fp.prefix(layer)
-                    _, sts = splitk_attention(q, pre, kc, vc, want_prefix=True)
-                    _, gscore = prefix_scores(q, pre, sts, torch.arange(t, dtype=torch.int32), value=True)
-                    gmp, glp, gop = (x[:, :1].cpu() for x in sts[:3])
+                    gmp, glp, gop = (x.cpu() for x in sts[:3])
                     rows = list(range(t))
-                    _, sscore = OA.prefix_scores(qc[:, :7], kd[:, :1], vd[:, :1].float(), gmp, glp, gop, rows,
+                    _, sscore = OA.prefix_scores(qc, kd, vd.float(), gmp, glp, gop, rows,
                                                  value_aware=True)
-                    _, wscore = OA.prefix_scores(qc[:, :7], kd[:, :1], vd[:, :1].float(), wmp, wlp, wop, rows,
+                    _, wscore = OA.prefix_scores(qc, kd, vd.float(), wmp, wlp, wop, rows,
                                                  value_aware=True)
-                    check_read_set(f"c4_seq{i}_n{n}_layer{layer}_head0", fp.states[layer].indices[:, :1].cpu(),
-                                   gscore[:, :1].cpu(), sscore, wscore, read_k)
+                    check_read_set(f"c4_seq{i}_n{n}_layer{layer}", fp.states[layer].indices.cpu(), gscore.cpu(), sscore,
+                                   wscore, read_k)
         # the lookahead eviction after step 0 (finish_step0): keep set on the GPU's scores
         pos0 = st.pos[..., :st.live].cpu().to(torch.int64)
         phys0 = st.phys[..., :st.live].cpu().to(torch.int64)
@@ -194,10 +202,9 @@ def test_config4_ragged_block_step(gpu):
                 assert torch.isfinite(out.float()).all()
                 if step == 1 and layer == L - 1 and check:
                     kd, vd = views[layer]
-                    gi = fp.states[layer].indices[:, :1].cpu().unsqueeze(-1).expand(-1, -1, -1, d)
-                    want = OA.dense_attention(q[:, :7].cpu(), kd[:, :1].gather(2, gi), vd[:, :1].gather(2, gi),
-                                              kc[:, :1].cpu(), vc[:, :1].cpu())
-                    assert_attention_close(out[:, :7], want)
+                    gi = fp.states[layer].indices.cpu().unsqueeze(-1).expand(-1, -1, -1, d)
+                    want = OA.dense_attention(q.cpu(), kd.gather(2, gi), vd.gather(2, gi), kc.cpu(), vc.cpu())
+                    assert_attention_close(out, want)
         # the block's finalize: its KV appended, its positions admitted
         cache.begin_append(t)
         for layer in range(L):
