@@ -764,12 +764,15 @@ def extra_c4_block(a, L=28, dense=2):
     """BASELINE config 4, the ragged multi-sequence full-model block step: 8 sequences with
     prefix lengths uniform in [8 192, 131 072] (seed 1234), 28 layers of the config-1 head
     shape (the first 2 dense), packed int4 KV (every whole group quantized), read 2 048 /
-    keep 4 096 per KV head.  Per sequence, from its freshly built cache, one block: step 0
-    of every layer (fast-path routing: split-K attention, value-aware scores with the
-    fused read-set select, gather), the lookahead eviction (keep score, keep set, packed
-    lazy rebuild), 3 denoising sub-steps and the block's finalize (its KV appended)
-    (session.py:1403-1454, 1985-2034, 270-361, 1286-1336, 2289-2297).  Launched op by op
-    from Python as the session runs it; the sequences one after another.  Algorithmic
+    keep 4 096 per KV head.  One block of the batch, from freshly built caches (one per
+    sequence): step 0 of every layer (fast-path routing: split-K attention, value-aware
+    scores with the fused read-set select, gather), the lookahead eviction (keep score,
+    keep set, packed lazy rebuild), 3 denoising sub-steps and the block's finalize (its KV
+    appended) (session.py:1403-1454, 1985-2034, 270-361, 1286-1336, 2289-2297).  Launched
+    op by op from Python as the session runs it, phase by phase as a batched forward does
+    (each layer's calls for every sequence in turn), so the host's launches of one
+    sequence overlap the GPU work of the others between the eviction's synchronisations.
+    Algorithmic
     bytes per sequence of prefix n (P = n x 4 KV heads x 160 B of int4 K and V with their
     scales): step 0 streams the prefix twice in a sparse layer (attention, scores) and once
     in a dense one; the eviction reads V once per layer (keep score) and reads and writes
@@ -787,55 +790,77 @@ def extra_c4_block(a, L=28, dense=2):
     cfg = EvictionConfig(policy="lookahead", recent_window=W, capacity_floor=512, compaction="lazy",
                          repack_below=1.0, sink_tokens=4)
 
-    def run(n, seed):
-        g = torch.Generator(device=dev).manual_seed(seed)
-        chan = torch.empty((1, hkv, 1, d), device=dev).log_normal_(0.0, 0.5, generator=g)
-        k = torch.randn((1, hkv, n, d), device=dev, generator=g) * chan
-        k[:, :, :4] *= 8.0
-        k = k.to(torch.bfloat16)
-        v = torch.randn((1, hkv, n, d), device=dev, generator=g).to(torch.bfloat16)
-        blocks = [tuple(x.to(torch.bfloat16) for x in (
-            torch.randn((1, hq, t, d), device=dev, generator=g),
-            torch.randn((1, hkv, t, d), device=dev, generator=g) * chan,
-            torch.randn((1, hkv, t, d), device=dev, generator=g))) for _ in range(L)]
-        cache = PackedKVCache(num_layers=L, batch_size=1, num_kv_heads=hkv, head_dim=d, max_tokens=n + 4 * t,
-                              quant=QuantizationConfig(residual_tokens=0), device=dev)
-        cache.begin_append(n)
-        for layer in range(L):
-            cache.stage_layer(layer, torch.roll(k, 977 * layer, dims=2), v)
-        cache.commit_append()
-        del k, v
-        st = EvictionState(num_layers=L, batch_size=1, num_kv_heads=hkv, capacity=n + 4 * t, device=dev)
-        st.append(range(n))
-        fp = FastLayerPath(cache=cache, block_size=t, query_indices=list(range(t)), dense_prefix_layers=dense)
+    class Seq:
+        """One sequence of the batch: its cache, eviction state, fast path and block inputs."""
+
+        def __init__(self, n, seed):
+            g = torch.Generator(device=dev).manual_seed(seed)
+            chan = torch.empty((1, hkv, 1, d), device=dev).log_normal_(0.0, 0.5, generator=g)
+            k = torch.randn((1, hkv, n, d), device=dev, generator=g) * chan
+            k[:, :, :4] *= 8.0
+            k = k.to(torch.bfloat16)
+            v = torch.randn((1, hkv, n, d), device=dev, generator=g).to(torch.bfloat16)
+            self.blocks = [tuple(x.to(torch.bfloat16) for x in (
+                torch.randn((1, hq, t, d), device=dev, generator=g),
+                torch.randn((1, hkv, t, d), device=dev, generator=g) * chan,
+                torch.randn((1, hkv, t, d), device=dev, generator=g))) for _ in range(L)]
+            self.cache = PackedKVCache(num_layers=L, batch_size=1, num_kv_heads=hkv, head_dim=d,
+                                       max_tokens=n + 4 * t, quant=QuantizationConfig(residual_tokens=0), device=dev)
+            self.cache.begin_append(n)
+            for layer in range(L):
+                self.cache.stage_layer(layer, torch.roll(k, 977 * layer, dims=2), v)
+            self.cache.commit_append()
+            del k, v
+            self.st = EvictionState(num_layers=L, batch_size=1, num_kv_heads=hkv, capacity=n + 4 * t, device=dev)
+            self.st.append(range(n))
+            self.fp = FastLayerPath(cache=self.cache, block_size=t, query_indices=list(range(t)),
+                                    dense_prefix_layers=dense)
+            self.n = n
+
+    def block_step(seqs):
+        """One block of the batch, phase by phase as a batched forward runs it: step 0 of
+        every layer (layer by layer, every sequence in turn), the lookahead eviction of every
+        sequence, 3 sub-steps (likewise), the finalize.  Returns the seconds it took."""
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        ctx = BlockContext(step_index=0, old_cache_len=n, topk=read_k, evicting=True, live_len=st.live,
-                           want_mass=True, live_slots={layer: st.phys[layer, ..., :st.live] for layer in range(L)})
+        for s in seqs:
+            s.ctx = BlockContext(step_index=0, old_cache_len=s.n, topk=read_k, evicting=True, live_len=s.st.live,
+                                 want_mass=True,
+                                 live_slots={layer: s.st.phys[layer, ..., :s.st.live] for layer in range(L)})
         for layer in range(L):
-            fp.route(layer, *blocks[layer], ctx)
-        lookahead_evict(cache, st, cfg, keep_k, fp.last_mass, None, next_position=n, check=False)
-        fp.slot_masks = live_slot_masks(cache, st)
+            for s in seqs:
+                s.fp.route(layer, *s.blocks[layer], s.ctx)
+        for s in seqs:
+            lookahead_evict(s.cache, s.st, cfg, keep_k, s.fp.last_mass, None, next_position=s.n, check=False)
+            s.fp.slot_masks = live_slot_masks(s.cache, s.st)
         for step in (1, 2, 3):
-            ctx.step_index = step
+            for s in seqs:
+                s.ctx.step_index = step
             for layer in range(L):
-                fp.route(layer, *blocks[layer], ctx)
-        cache.begin_append(t)
-        for layer in range(L):
-            cache.stage_layer(layer, blocks[layer][1], blocks[layer][2])
-        cache.commit_append()
-        st.append(range(n, n + t))
+                for s in seqs:
+                    s.fp.route(layer, *s.blocks[layer], s.ctx)
+        for s in seqs:
+            s.cache.begin_append(t)
+            for layer in range(L):
+                s.cache.stage_layer(layer, s.blocks[layer][1], s.blocks[layer][2])
+            s.cache.commit_append()
+            s.st.append(range(s.n, s.n + t))
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
-        cache.check_rebuild()                            # the eviction's deferred error status
-        del cache, st, fp, blocks
+        for s in seqs:
+            s.cache.check_rebuild()                      # the eviction's deferred error status
         return sec
 
-    # warm-up at the longest prefix: kernels loaded, and torch's caching allocator grown to
-    # the largest sequence's footprint, so the timed sequences reuse its blocks as a serving
-    # process does (a cold allocator's device allocations synchronize the host)
-    run(max(lens), 999)
-    secs = [run(n, 1234 + i) for i, n in enumerate(lens)]
+    # warm-up: the same batch once (kernels loaded, and torch's caching allocator grown to
+    # the batch's footprint, so the timed block reuses its blocks as a serving process does:
+    # a cold allocator's device allocations synchronize the host); then fresh caches
+    seqs = [Seq(n, 1234 + i) for i, n in enumerate(lens)]
+    block_step(seqs)
+    del seqs
+    seqs = [Seq(n, 1234 + i) for i, n in enumerate(lens)]
+    sec = block_step(seqs)
+    del seqs
+    torch.cuda.empty_cache()
     r = (hq // hkv) * t
     nbytes = flops = 0
     for n in lens:
@@ -845,12 +870,10 @@ def extra_c4_block(a, L=28, dense=2):
         nbytes += 3 * ((L - dense) * read_k * hkv * d * 2 * 2 + dense * keep_k * hkv * 160)   # sub-steps
         flops += (L - dense) * 6 * r * n * d * hkv + dense * 4 * r * n * d * hkv
         flops += 3 * ((L - dense) * 4 * r * read_k * d * hkv + dense * 4 * r * keep_k * d * hkv)
-    sec = sum(secs)
     return {"workload": f"c4: 8 sequences, prefixes {sorted(lens)}, 28 layers ({dense} dense), packed int4, "
-                        f"read {read_k} / keep {keep_k}: step 0 + lookahead eviction + 3 sub-steps + finalize per "
-                        f"sequence, eager, sequences one after another",
-            "us_per_block_step": round(sec * 1e6, 1),
-            "us_per_sequence": [round(x * 1e6, 1) for x in secs], "roofline": _roof(nbytes, flops, sec)}
+                        f"read {read_k} / keep {keep_k}: one block of the batch -- step 0 of every layer, the "
+                        f"lookahead eviction, 3 sub-steps, the finalize -- eager, phase by phase over the sequences",
+            "us_per_block_step": round(sec * 1e6, 1), "roofline": _roof(nbytes, flops, sec)}
 
 
 def extra_evict(a):

@@ -287,6 +287,19 @@ int ma_quantize_keys(ma_tensor4 src, int B, int H, int T, int D, int group, void
                      const int64_t skq[4], void *ks, void *kz, const int64_t sks[3], void *stream);
 int ma_quantize_values(ma_tensor4 src, int B, int H, int T, int D, int group, void *vq,
                        const int64_t svq[4], void *vs, void *vz, const int64_t svs[3], void *stream);
+/* PackedKVCache.stage_layer of a packed store (cache.py:423-548, with the plan of
+ * begin_append, 385-421): over the token axis [k_res rows 0..old_res | k_new rows 0..T) (and the
+ * same for V), the first `move` tokens (a multiple of 32) are quantized as
+ * ma_quantize_keys / ma_quantize_values do into planes kq/ks/kz and vq/vs/vz whose first
+ * group / row is where they go, and the remaining keep = old_res + T - move tokens are
+ * written to the residual rows 0..keep (in place: its rows move down by `move`).  The
+ * residual and the new tokens share one dtype (the quantizers' rule follows it), as the
+ * reference's [residual | new.to(compute dtype)] tensor does.  Up to three launches,
+ * no temporary. */
+int ma_append_packed(ma_tensor4 k_res, ma_tensor4 v_res, int old_res, ma_tensor4 k_new, ma_tensor4 v_new, int B,
+                     int H, int T, int D, int move, int keep, void *kq, const int64_t skq[4], void *ks, void *kz,
+                     const int64_t sks[3], void *vq, const int64_t svq[4], void *vs, void *vz,
+                     const int64_t svs[3], void *stream);
 
 /* f1. packed eviction rebuild, plan half: the lists of the session's lazy / full
  * compaction (runtime/session.py:288-345, BitSieveSession._evict_to) for `lanes`

@@ -92,6 +92,8 @@ SIGNATURES = {
     "ma_gather_kv": (_I, [_PREF, _I, _I, _I, _P, _I64P, _I, _T4, _T4, _P]),
     "ma_quantize_keys": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),
     "ma_quantize_values": (_I, [_T4, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P]),
+    "ma_append_packed": (_I, [_T4, _T4, _I, _T4, _T4, _I, _I, _I, _I, _I, _I, _P, _I64P, _P, _P, _I64P, _P, _I64P,
+                              _P, _P, _I64P, _P]),
     "ma_rebuild_plan": (_I, [_P, _I64, _P, _I, _I64, _I, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P]),
     "ma_rebuild_packed": (_I, [_PREF, _I, _I, _I, _PREF, _P, _I64, _I, _P, _I64, _I, _P, _I64, _I, _P, _I64, _I,
                                _P, _I64, _P, _I64, _I, _P, _P]),

@@ -285,7 +285,9 @@ class PackedKVCache:
             append_tokens(key, self.k_fp[layer_idx], plan.old_length)
         if self.v_fp is not None:
             append_tokens(value, self.v_fp[layer_idx], plan.old_length)
-        if self.quant.packed:
+        if self.quant.packed and self._append_fused(key, value):
+            self._append_packed(layer_idx, plan, key, value)
+        elif self.quant.packed:
             move, keep = plan.quantize_from_residual, plan.new_residual
             k_tail = self._tail(self.k_residual[layer_idx], plan.old_residual, key)
             v_tail = self._tail(self.v_residual[layer_idx], plan.old_residual, value)
@@ -304,6 +306,29 @@ class PackedKVCache:
                 append_tokens(k_tail[:, :, move:], self.k_residual[layer_idx], 0)
                 append_tokens(v_tail[:, :, move:], self.v_residual[layer_idx], 0)
         plan.staged_layers.add(layer_idx)
+
+    def _append_fused(self, key: torch.Tensor, value: torch.Tensor) -> bool:
+        """Whether ma_append_packed serves this append: new tokens in the compute dtype (so
+        [residual | new] needs no conversion), the built 4-bit widths and groups."""
+        q = self.quant
+        return (key.dtype == self.compute_dtype and value.dtype == self.compute_dtype and key.stride(-1) == 1
+                and value.stride(-1) == 1 and q.k_bits == 4 and q.v_bits == 4 and q.key_token_group == 32
+                and q.value_channel_group == 32 and self.k_fp is None and self.v_fp is None)
+
+    def _append_packed(self, layer_idx: int, plan: "AppendPlan", key: torch.Tensor, value: torch.Tensor) -> None:
+        """One layer's packed append in one ma_append_packed call: the whole key groups of
+        [residual | new] quantized into the planes after the quantized part, the rest left
+        as the residual (the same bytes as the quantizers over the concatenated tail)."""
+        move, keep = plan.quantize_from_residual, plan.new_residual
+        g0, t0 = self.quantized_length // self.quant.key_token_group, self.quantized_length
+        kq, ks, kz = (x[layer_idx, :, :, g0:] for x in (self.k_q, self.k_scale, self.k_zero))
+        vq, vs, vz = (x[layer_idx, :, :, t0:] for x in (self.v_q, self.v_scale, self.v_zero))
+        b, h, t, d = key.shape
+        N.call("ma_append_packed", N.t4(self.k_residual[layer_idx]), N.t4(self.v_residual[layer_idx]),
+               plan.old_residual, N.t4(key), N.t4(value), b, h, t, d, move, keep, kq.data_ptr(),
+               N.i64arr(*kq.stride()[:4]), ks.data_ptr(), kz.data_ptr(), N.i64arr(*ks.stride()[:3]), vq.data_ptr(),
+               N.i64arr(*vq.stride()[:4]), vs.data_ptr(), vz.data_ptr(), N.i64arr(*vs.stride()[:3]),
+               N.stream_of(key))
 
     def _tail(self, residual: torch.Tensor, old: int, new: torch.Tensor) -> torch.Tensor:
         """[residual rows 0..old | new] as one compute-dtype tensor (a copy when old > 0)."""

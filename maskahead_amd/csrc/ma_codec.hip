@@ -190,8 +190,25 @@ __global__ void __launch_bounds__(256) gather_kernel(PrefixArgs a, int H, int D,
 }
 
 // ---------------------------------------------------------------- quantizers
+// The source of a quantizer: token rows 0 .. na-1 from `a`, the rest from `b` (row i - na)
+// -- [residual | new tokens] of an append without building that tensor; na = 0 reads `b`
+// alone.  a and b have the same dtype.
+struct TwoSrc {
+    ma_tensor4 a, b;
+    int na;
+};
+
+__device__ __forceinline__ float two_load(const TwoSrc &s, int b, int h, int i, int d) {
+    const bool in_a = i < s.na;
+    const char *base = (const char *)(in_a ? s.a.ptr : s.b.ptr);
+    const int64_t sb = in_a ? s.a.s[0] : s.b.s[0], sh = in_a ? s.a.s[1] : s.b.s[1],
+                  st = in_a ? s.a.s[2] : s.b.s[2];
+    const int r = in_a ? i : i - s.na;
+    return ma_load_f(base, b * sb + h * sh + (int64_t)r * st + d, s.b.dtype);
+}
+
 // keys: grid (T/KG, B*H), D threads; thread = one channel of one token group.
-__global__ void quantize_keys_kernel(ma_tensor4 src, int H, int D, uint8_t *kq, int64_t q0, int64_t q1, int64_t q2,
+__global__ void quantize_keys_kernel(TwoSrc src, int H, int D, uint8_t *kq, int64_t q0, int64_t q1, int64_t q2,
                                      int64_t q3, _Float16 *ks, _Float16 *kz, int64_t s0, int64_t s1, int64_t s2) {
     const int bh = blockIdx.y, b = bh / H, h = bh % H;
     const int g = blockIdx.x;
@@ -201,14 +218,15 @@ __global__ void quantize_keys_kernel(ma_tensor4 src, int H, int D, uint8_t *kq, 
     float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int t = 0; t < KG; ++t) {
-        x[t] = ma_load_f(src.ptr, b * src.s[0] + h * src.s[1] + (int64_t)(g * KG + t) * src.s[2] + d, src.dtype);
+        x[t] = two_load(src, b, h, g * KG + t, d);
         lo = fminf(lo, x[t]);
         hi = fmaxf(hi, x[t]);
     }
-    QuantGroup qp = quant_params(lo, hi, src.dtype);
+    const int dtype = src.b.dtype;
+    QuantGroup qp = quant_params(lo, hi, dtype);
     uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int t = 0; t < KG; ++t) w[t >> 3] |= quant_code(x[t], qp, src.dtype) << ((t & 7) * 4);
+    for (int t = 0; t < KG; ++t) w[t >> 3] |= quant_code(x[t], qp, dtype) << ((t & 7) * 4);
     uint4 out = {w[0], w[1], w[2], w[3]};
     *(uint4 *)(kq + b * q0 + h * q1 + (int64_t)g * q2 + (int64_t)d * q3) = out;
     int64_t so = b * s0 + h * s1 + (int64_t)g * s2 + d;
@@ -217,12 +235,13 @@ __global__ void quantize_keys_kernel(ma_tensor4 src, int H, int D, uint8_t *kq, 
 }
 
 // values: one thread per (token, channel group); grid-stride over B*H*T*(D/VG) items.
-__global__ void __launch_bounds__(256) quantize_values_kernel(ma_tensor4 src, int BH, int H, int T, int D, uint8_t *vq,
+__global__ void __launch_bounds__(256) quantize_values_kernel(TwoSrc src, int BH, int H, int T, int D, uint8_t *vq,
                                                               int64_t q0, int64_t q1, int64_t q2, int64_t q3,
                                                               _Float16 *vs, _Float16 *vz, int64_t s0, int64_t s1,
                                                               int64_t s2) {
     const int ncg = D / VG;
     const int64_t total = (int64_t)BH * T * ncg;
+    const int dtype = src.b.dtype;
     for (int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x; it < total; it += (int64_t)gridDim.x * 256) {
         int cg = (int)(it % ncg);
         int64_t rest = it / ncg;
@@ -230,22 +249,53 @@ __global__ void __launch_bounds__(256) quantize_values_kernel(ma_tensor4 src, in
         int bh = (int)(rest / T), b = bh / H, h = bh % H;
         float x[VG];
         float lo = INFINITY, hi = -INFINITY;
-        int64_t base = b * src.s[0] + h * src.s[1] + (int64_t)j * src.s[2] + cg * VG;
 #pragma unroll
         for (int c = 0; c < VG; ++c) {
-            x[c] = ma_load_f(src.ptr, base + c, src.dtype);
+            x[c] = two_load(src, b, h, j, cg * VG + c);
             lo = fminf(lo, x[c]);
             hi = fmaxf(hi, x[c]);
         }
-        QuantGroup qp = quant_params(lo, hi, src.dtype);
+        QuantGroup qp = quant_params(lo, hi, dtype);
         uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int c = 0; c < VG; ++c) w[c >> 3] |= quant_code(x[c], qp, src.dtype) << ((c & 7) * 4);
+        for (int c = 0; c < VG; ++c) w[c >> 3] |= quant_code(x[c], qp, dtype) << ((c & 7) * 4);
         uint4 out = {w[0], w[1], w[2], w[3]};
         *(uint4 *)(vq + b * q0 + h * q1 + (int64_t)j * q2 + (int64_t)cg * q3) = out;
         int64_t so = b * s0 + h * s1 + (int64_t)j * s2 + cg;
         vs[so] = (_Float16)qp.step;
         vz[so] = (_Float16)qp.lo;
+    }
+}
+
+// The residual an append keeps: token rows [move, na + T) of [a | b] into a's rows
+// [0, keep), for K (blockIdx.y 0) and V (1).  Rows of a move down by `move` in place, so
+// one workgroup per lane copies them in chunks of CH rows, every chunk read whole before
+// any of it is written: a chunk's destination rows lie below the source rows of every
+// later chunk.  (move = 0 leaves a's rows where they are and appends b's.)
+constexpr int RK_NT = 256;
+__global__ void __launch_bounds__(RK_NT) residual_keep_kernel(TwoSrc k, TwoSrc v, int H, int D, int move, int keep) {
+    const TwoSrc &s = blockIdx.y ? v : k;
+    const int bh = blockIdx.x, b = bh / H, h = bh % H;
+    const int first = move == 0 ? s.na : 0;      // move = 0: a's rows stay, b's follow them
+    const int per = RK_NT / D;                   // rows per pass of the workgroup
+    const int r0 = threadIdx.x / D, d = threadIdx.x % D;
+    constexpr int RPT = 8;                       // rows per thread per chunk
+    char *dst = (char *)s.a.ptr;
+    for (int c0 = first; c0 < keep; c0 += per * RPT) {
+        float x[RPT];
+#pragma unroll
+        for (int e = 0; e < RPT; ++e) {
+            const int r = c0 + e * per + r0;
+            x[e] = r < keep && r0 < per ? two_load(s, b, h, r + move, d) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < RPT; ++e) {
+            const int r = c0 + e * per + r0;
+            if (r < keep && r0 < per)
+                ma_store_f(dst, b * s.a.s[0] + h * s.a.s[1] + (int64_t)r * s.a.s[2] + d, s.a.dtype, x[e]);
+        }
+        __syncthreads();
     }
 }
 
@@ -359,7 +409,8 @@ extern "C" int ma_quantize_keys(ma_tensor4 src, int B, int H, int T, int D, int 
     }
     if (T == 0) return MA_OK;
     dim3 grid(T / KG, B * H);
-    hipLaunchKernelGGL(quantize_keys_kernel, grid, dim3(D), 0, (hipStream_t)stream, src, H, D, (uint8_t *)kq, skq[0],
+    const TwoSrc two{src, src, 0};
+    hipLaunchKernelGGL(quantize_keys_kernel, grid, dim3(D), 0, (hipStream_t)stream, two, H, D, (uint8_t *)kq, skq[0],
                        skq[1], skq[2], skq[3], (_Float16 *)ks, (_Float16 *)kz, sks[0], sks[1], sks[2]);
     return ma_check_launch("ma_quantize_keys");
 }
@@ -379,8 +430,54 @@ extern "C" int ma_quantize_values(ma_tensor4 src, int B, int H, int T, int D, in
     int64_t items = (int64_t)B * H * T * (D / VG);
     int blocks = (int)((items + 255) / 256);
     if (blocks > 65535) blocks = 65535;
-    hipLaunchKernelGGL(quantize_values_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, src, B * H, H, T, D,
+    const TwoSrc two{src, src, 0};
+    hipLaunchKernelGGL(quantize_values_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, two, B * H, H, T, D,
                        (uint8_t *)vq, svq[0], svq[1], svq[2], svq[3], (_Float16 *)vs, (_Float16 *)vz, svs[0], svs[1],
                        svs[2]);
     return ma_check_launch("ma_quantize_values");
+}
+
+extern "C" int ma_append_packed(ma_tensor4 k_res, ma_tensor4 v_res, int old_res, ma_tensor4 k_new, ma_tensor4 v_new,
+                                int B, int H, int T, int D, int move, int keep, void *kq, const int64_t skq[4],
+                                void *ks, void *kz, const int64_t sks[3], void *vq, const int64_t svq[4], void *vs,
+                                void *vz, const int64_t svs[3], void *stream) {
+    const char *who = "ma_append_packed";
+    if (B <= 0 || H <= 0 || T <= 0 || old_res < 0 || move < 0 || keep < 0 || move % KG || move + keep != old_res + T ||
+        D <= 0 || D % VG || D > RK_NT || RK_NT % D || !k_new.ptr || !v_new.ptr ||
+        ((old_res > 0 || keep > 0) && (!k_res.ptr || !v_res.ptr))) {
+        ma_set_error("%s: bad geometry (move %% 32, move + keep = old_res + T, D | 256)", who);
+        return MA_EINVAL;
+    }
+    if (k_new.dtype != v_new.dtype || !out_dtype_ok(k_new.dtype) ||
+        ((old_res > 0 || keep > 0) && (k_res.dtype != k_new.dtype || v_res.dtype != k_new.dtype))) {
+        ma_set_error("%s: the residual and the new tokens must share one 16-bit or f32 dtype", who);
+        return MA_EINVAL;
+    }
+    const TwoSrc tk{k_res, k_new, old_res}, tv{v_res, v_new, old_res};
+    if (move) {
+        if (!kq || !ks || !kz || !skq || !sks || !vq || !vs || !vz || !svq || !svs || ((uintptr_t)kq & 15) ||
+            ((uintptr_t)vq & 15) || ((skq[2] | skq[3] | svq[2] | svq[3]) & 15)) {
+            ma_set_error("%s: packed planes missing or payload rows not 16-byte aligned", who);
+            return MA_EINVAL;
+        }
+        hipLaunchKernelGGL(quantize_keys_kernel, dim3(move / KG, B * H), dim3(D), 0, (hipStream_t)stream, tk, H, D,
+                           (uint8_t *)kq, skq[0], skq[1], skq[2], skq[3], (_Float16 *)ks, (_Float16 *)kz, sks[0],
+                           sks[1], sks[2]);
+        int rc = ma_check_launch(who);
+        if (rc) return rc;
+        const int64_t items = (int64_t)B * H * move * (D / VG);
+        int blocks = (int)((items + 255) / 256);
+        if (blocks > 65535) blocks = 65535;
+        hipLaunchKernelGGL(quantize_values_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, tv, B * H, H,
+                           move, D, (uint8_t *)vq, svq[0], svq[1], svq[2], svq[3], (_Float16 *)vs, (_Float16 *)vz,
+                           svs[0], svs[1], svs[2]);
+        rc = ma_check_launch(who);
+        if (rc) return rc;
+    }
+    if (keep > (move ? 0 : old_res)) {
+        hipLaunchKernelGGL(residual_keep_kernel, dim3(B * H, 2), dim3(RK_NT), 0, (hipStream_t)stream, tk, tv, H, D,
+                           move, keep);
+        return ma_check_launch(who);
+    }
+    return MA_OK;
 }

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+from maskahead_amd.cache import PackedKVCache
 from maskahead_amd.eviction import EvictionConfig, EvictionState
 from maskahead_amd.kernels import gather_packed_kv
 from maskahead_amd.kernels.keep import append_tokens, compact_tokens, keep_select, value_score, value_score_slots
@@ -221,3 +222,44 @@ def test_append_tokens(gpu):
     assert torch.equal(dg.cpu(), want)
     with pytest.raises(ValueError):
         append_tokens(src.to(gpu), dg, 80)                  # past the capacity
+
+
+@pytest.mark.parametrize("residual_tokens", [0, 32, 64])
+def test_fused_packed_append_equals_quantizer_path(gpu, residual_tokens):
+    """PackedKVCache.stage_layer through ma_append_packed (one call: quantize from
+    [residual | new] directly, then the residual shifted down in place) writes the same
+    bytes as the path that builds [residual | new] and calls the quantizers and the append
+    kernel (the reference's stage_layer, cache.py:423-548), over appends that hit every
+    case: new tokens only appended to the residual, whole groups quantized with the kept
+    residual moving down over rows it is read from, and a long prefill.  The quantizer path
+    itself is pinned against the oracle and the reference's golden vectors."""
+    from maskahead_amd.config import QuantizationConfig
+
+    g = torch.Generator().manual_seed(71)
+    L, B, H, D = 2, 2, 3, 128
+    quant = QuantizationConfig(residual_tokens=residual_tokens)
+    caches = [PackedKVCache(num_layers=L, batch_size=B, num_kv_heads=H, head_dim=D, max_tokens=4096, quant=quant,
+                            device=gpu) for _ in range(2)]
+    caches[1]._append_fused = lambda key, value: False        # the quantizer path
+    names = ("k_q", "k_scale", "k_zero", "v_q", "v_scale", "v_zero", "k_residual", "v_residual")
+    seen = set()
+    for n in (300, 32, 32, 7, 32, 32, 25, 32, 64, 32):
+        kv = [(torch.randn((B, H, n, D), generator=g) * 3).to(torch.bfloat16) for _ in range(2 * L)]
+        for c in caches:
+            plan = c.begin_append(n)
+            for layer in range(L):
+                c.stage_layer(layer, kv[2 * layer].to(gpu), kv[2 * layer + 1].to(gpu))
+            c.commit_append()
+        seen.add((plan.quantize_from_residual > 0, plan.quantize_from_residual < plan.old_residual,
+                  plan.new_residual > 0))
+        a, b = caches
+        assert (a.length, a.quantized_length, a.residual_length) == (b.length, b.quantized_length, b.residual_length)
+        ql, rl = a.quantized_length, a.residual_length
+        for name in names:
+            x, y = getattr(a, name), getattr(b, name)
+            cut = ql // 32 if name.startswith("k_") and "residual" not in name else ql if "residual" not in name \
+                else rl
+            assert torch.equal(x[:, :, :, :cut].cpu(), y[:, :, :, :cut].cpu()), (n, name)
+    if residual_tokens:
+        # the in-place shift over its own source rows and the append-only case both ran
+        assert (True, True, True) in seen and (False, True, True) in seen
