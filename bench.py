@@ -771,7 +771,8 @@ def extra_c4_block(a, L=28, dense=2):
     appended) (session.py:1403-1454, 1985-2034, 270-361, 1286-1336, 2289-2297).  Launched
     op by op from Python as the session runs it, phase by phase as a batched forward does
     (each layer's calls for every sequence in turn), so the host's launches of one
-    sequence overlap the GPU work of the others between the eviction's synchronisations.
+    sequence overlap the GPU work of the others; the evictions of the batch read their
+    plans' counts back in one synchronisation (lookahead_evict_batch).
     Algorithmic
     bytes per sequence of prefix n (P = n x 4 KV heads x 160 B of int4 K and V with their
     scales): step 0 streams the prefix twice in a sparse layer (attention, scores) and once
@@ -782,7 +783,7 @@ def extra_c4_block(a, L=28, dense=2):
     from maskahead_amd.config import QuantizationConfig
     from maskahead_amd.eviction import EvictionConfig, EvictionState
     from maskahead_amd.runtime.fastpath import BlockContext, FastLayerPath
-    from maskahead_amd.runtime.session import live_slot_masks, lookahead_evict
+    from maskahead_amd.runtime.session import live_slot_masks, lookahead_evict_batch
 
     dev = torch.device("cuda:0")
     hq, hkv, d, t, read_k, keep_k, W = 28, 4, 128, 32, 2048, 4096, 64
@@ -824,14 +825,15 @@ def extra_c4_block(a, L=28, dense=2):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for s in seqs:
+            # step 0 keeps each layer's mass per physical slot; the eviction puts all layers'
+            # in live order at once (lookahead_scores, per_slot)
             s.ctx = BlockContext(step_index=0, old_cache_len=s.n, topk=read_k, evicting=True, live_len=s.st.live,
-                                 want_mass=True,
-                                 live_slots={layer: s.st.phys[layer, ..., :s.st.live] for layer in range(L)})
+                                 want_mass=True)
         for layer in range(L):
             for s in seqs:
                 s.fp.route(layer, *s.blocks[layer], s.ctx)
+        lookahead_evict_batch([(s.cache, s.st, s.fp.last_mass, None, s.n) for s in seqs], cfg, keep_k, per_slot=True)
         for s in seqs:
-            lookahead_evict(s.cache, s.st, cfg, keep_k, s.fp.last_mass, None, next_position=s.n, check=False)
             s.fp.slot_masks = live_slot_masks(s.cache, s.st)
         for step in (1, 2, 3):
             for s in seqs:

@@ -198,16 +198,20 @@ struct TwoSrc {
     int na;
 };
 
+// DT: the dtype, a compile-time constant so that a thread's loads are straight-line code
+// (all of them in flight at once) instead of one branch per element
+template <int DT>
 __device__ __forceinline__ float two_load(const TwoSrc &s, int b, int h, int i, int d) {
     const bool in_a = i < s.na;
     const char *base = (const char *)(in_a ? s.a.ptr : s.b.ptr);
     const int64_t sb = in_a ? s.a.s[0] : s.b.s[0], sh = in_a ? s.a.s[1] : s.b.s[1],
                   st = in_a ? s.a.s[2] : s.b.s[2];
     const int r = in_a ? i : i - s.na;
-    return ma_load_f(base, b * sb + h * sh + (int64_t)r * st + d, s.b.dtype);
+    return ma_load_f(base, b * sb + h * sh + (int64_t)r * st + d, DT);
 }
 
 // keys: grid (T/KG, B*H), D threads; thread = one channel of one token group.
+template <int DT>
 __global__ void quantize_keys_kernel(TwoSrc src, int H, int D, uint8_t *kq, int64_t q0, int64_t q1, int64_t q2,
                                      int64_t q3, _Float16 *ks, _Float16 *kz, int64_t s0, int64_t s1, int64_t s2) {
     const int bh = blockIdx.y, b = bh / H, h = bh % H;
@@ -218,11 +222,11 @@ __global__ void quantize_keys_kernel(TwoSrc src, int H, int D, uint8_t *kq, int6
     float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
     for (int t = 0; t < KG; ++t) {
-        x[t] = two_load(src, b, h, g * KG + t, d);
+        x[t] = two_load<DT>(src, b, h, g * KG + t, d);
         lo = fminf(lo, x[t]);
         hi = fmaxf(hi, x[t]);
     }
-    const int dtype = src.b.dtype;
+    constexpr int dtype = DT;
     QuantGroup qp = quant_params(lo, hi, dtype);
     uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -235,13 +239,14 @@ __global__ void quantize_keys_kernel(TwoSrc src, int H, int D, uint8_t *kq, int6
 }
 
 // values: one thread per (token, channel group); grid-stride over B*H*T*(D/VG) items.
+template <int DT>
 __global__ void __launch_bounds__(256) quantize_values_kernel(TwoSrc src, int BH, int H, int T, int D, uint8_t *vq,
                                                               int64_t q0, int64_t q1, int64_t q2, int64_t q3,
                                                               _Float16 *vs, _Float16 *vz, int64_t s0, int64_t s1,
                                                               int64_t s2) {
     const int ncg = D / VG;
     const int64_t total = (int64_t)BH * T * ncg;
-    const int dtype = src.b.dtype;
+    constexpr int dtype = DT;
     for (int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x; it < total; it += (int64_t)gridDim.x * 256) {
         int cg = (int)(it % ncg);
         int64_t rest = it / ncg;
@@ -251,7 +256,7 @@ __global__ void __launch_bounds__(256) quantize_values_kernel(TwoSrc src, int BH
         float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
         for (int c = 0; c < VG; ++c) {
-            x[c] = two_load(src, b, h, j, cg * VG + c);
+            x[c] = two_load<DT>(src, b, h, j, cg * VG + c);
             lo = fminf(lo, x[c]);
             hi = fmaxf(hi, x[c]);
         }
@@ -273,6 +278,7 @@ __global__ void __launch_bounds__(256) quantize_values_kernel(TwoSrc src, int BH
 // any of it is written: a chunk's destination rows lie below the source rows of every
 // later chunk.  (move = 0 leaves a's rows where they are and appends b's.)
 constexpr int RK_NT = 256;
+template <int DT>
 __global__ void __launch_bounds__(RK_NT) residual_keep_kernel(TwoSrc k, TwoSrc v, int H, int D, int move, int keep) {
     const TwoSrc &s = blockIdx.y ? v : k;
     const int bh = blockIdx.x, b = bh / H, h = bh % H;
@@ -286,17 +292,45 @@ __global__ void __launch_bounds__(RK_NT) residual_keep_kernel(TwoSrc k, TwoSrc v
 #pragma unroll
         for (int e = 0; e < RPT; ++e) {
             const int r = c0 + e * per + r0;
-            x[e] = r < keep && r0 < per ? two_load(s, b, h, r + move, d) : 0.f;
+            x[e] = r < keep && r0 < per ? two_load<DT>(s, b, h, r + move, d) : 0.f;
         }
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < RPT; ++e) {
             const int r = c0 + e * per + r0;
             if (r < keep && r0 < per)
-                ma_store_f(dst, b * s.a.s[0] + h * s.a.s[1] + (int64_t)r * s.a.s[2] + d, s.a.dtype, x[e]);
+                ma_store_f(dst, b * s.a.s[0] + h * s.a.s[1] + (int64_t)r * s.a.s[2] + d, DT, x[e]);
         }
         __syncthreads();
     }
+}
+
+template <int DT>
+void quant_keys_as(dim3 grid, int D, hipStream_t st, const TwoSrc &src, int H, void *kq, const int64_t *skq, void *ks,
+                   void *kz, const int64_t *sks) {
+    hipLaunchKernelGGL(quantize_keys_kernel<DT>, grid, dim3(D), 0, st, src, H, D, (uint8_t *)kq, skq[0], skq[1], skq[2],
+                       skq[3], (_Float16 *)ks, (_Float16 *)kz, sks[0], sks[1], sks[2]);
+}
+
+void launch_quant_keys(int dtype, dim3 grid, int D, hipStream_t st, const TwoSrc &src, int H, void *kq,
+                       const int64_t *skq, void *ks, void *kz, const int64_t *sks) {
+    if (dtype == MA_BF16) quant_keys_as<MA_BF16>(grid, D, st, src, H, kq, skq, ks, kz, sks);
+    else if (dtype == MA_F16) quant_keys_as<MA_F16>(grid, D, st, src, H, kq, skq, ks, kz, sks);
+    else quant_keys_as<MA_F32>(grid, D, st, src, H, kq, skq, ks, kz, sks);
+}
+
+template <int DT>
+void quant_values_as(int blocks, hipStream_t st, const TwoSrc &src, int BH, int H, int T, int D, void *vq,
+                     const int64_t *svq, void *vs, void *vz, const int64_t *svs) {
+    hipLaunchKernelGGL(quantize_values_kernel<DT>, dim3(blocks), dim3(256), 0, st, src, BH, H, T, D, (uint8_t *)vq,
+                       svq[0], svq[1], svq[2], svq[3], (_Float16 *)vs, (_Float16 *)vz, svs[0], svs[1], svs[2]);
+}
+
+void launch_quant_values(int dtype, int blocks, hipStream_t st, const TwoSrc &src, int BH, int H, int T, int D,
+                         void *vq, const int64_t *svq, void *vs, void *vz, const int64_t *svs) {
+    if (dtype == MA_BF16) quant_values_as<MA_BF16>(blocks, st, src, BH, H, T, D, vq, svq, vs, vz, svs);
+    else if (dtype == MA_F16) quant_values_as<MA_F16>(blocks, st, src, BH, H, T, D, vq, svq, vs, vz, svs);
+    else quant_values_as<MA_F32>(blocks, st, src, BH, H, T, D, vq, svq, vs, vz, svs);
 }
 
 }  // namespace
@@ -410,8 +444,7 @@ extern "C" int ma_quantize_keys(ma_tensor4 src, int B, int H, int T, int D, int 
     if (T == 0) return MA_OK;
     dim3 grid(T / KG, B * H);
     const TwoSrc two{src, src, 0};
-    hipLaunchKernelGGL(quantize_keys_kernel, grid, dim3(D), 0, (hipStream_t)stream, two, H, D, (uint8_t *)kq, skq[0],
-                       skq[1], skq[2], skq[3], (_Float16 *)ks, (_Float16 *)kz, sks[0], sks[1], sks[2]);
+    launch_quant_keys(src.dtype, grid, D, (hipStream_t)stream, two, H, kq, skq, ks, kz, sks);
     return ma_check_launch("ma_quantize_keys");
 }
 
@@ -431,9 +464,7 @@ extern "C" int ma_quantize_values(ma_tensor4 src, int B, int H, int T, int D, in
     int blocks = (int)((items + 255) / 256);
     if (blocks > 65535) blocks = 65535;
     const TwoSrc two{src, src, 0};
-    hipLaunchKernelGGL(quantize_values_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, two, B * H, H, T, D,
-                       (uint8_t *)vq, svq[0], svq[1], svq[2], svq[3], (_Float16 *)vs, (_Float16 *)vz, svs[0], svs[1],
-                       svs[2]);
+    launch_quant_values(src.dtype, blocks, (hipStream_t)stream, two, B * H, H, T, D, vq, svq, vs, vz, svs);
     return ma_check_launch("ma_quantize_values");
 }
 
@@ -460,23 +491,27 @@ extern "C" int ma_append_packed(ma_tensor4 k_res, ma_tensor4 v_res, int old_res,
             ma_set_error("%s: packed planes missing or payload rows not 16-byte aligned", who);
             return MA_EINVAL;
         }
-        hipLaunchKernelGGL(quantize_keys_kernel, dim3(move / KG, B * H), dim3(D), 0, (hipStream_t)stream, tk, H, D,
-                           (uint8_t *)kq, skq[0], skq[1], skq[2], skq[3], (_Float16 *)ks, (_Float16 *)kz, sks[0],
-                           sks[1], sks[2]);
+        launch_quant_keys(k_new.dtype, dim3(move / KG, B * H), D, (hipStream_t)stream, tk, H, kq, skq, ks, kz, sks);
         int rc = ma_check_launch(who);
         if (rc) return rc;
         const int64_t items = (int64_t)B * H * move * (D / VG);
         int blocks = (int)((items + 255) / 256);
         if (blocks > 65535) blocks = 65535;
-        hipLaunchKernelGGL(quantize_values_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, tv, B * H, H,
-                           move, D, (uint8_t *)vq, svq[0], svq[1], svq[2], svq[3], (_Float16 *)vs, (_Float16 *)vz,
-                           svs[0], svs[1], svs[2]);
+        launch_quant_values(k_new.dtype, blocks, (hipStream_t)stream, tv, B * H, H, move, D, vq, svq, vs, vz, svs);
         rc = ma_check_launch(who);
         if (rc) return rc;
     }
     if (keep > (move ? 0 : old_res)) {
-        hipLaunchKernelGGL(residual_keep_kernel, dim3(B * H, 2), dim3(RK_NT), 0, (hipStream_t)stream, tk, tv, H, D,
-                           move, keep);
+        const dim3 grid(B * H, 2);
+        if (k_new.dtype == MA_BF16)
+            hipLaunchKernelGGL(residual_keep_kernel<MA_BF16>, grid, dim3(RK_NT), 0, (hipStream_t)stream, tk, tv, H, D,
+                               move, keep);
+        else if (k_new.dtype == MA_F16)
+            hipLaunchKernelGGL(residual_keep_kernel<MA_F16>, grid, dim3(RK_NT), 0, (hipStream_t)stream, tk, tv, H, D,
+                               move, keep);
+        else
+            hipLaunchKernelGGL(residual_keep_kernel<MA_F32>, grid, dim3(RK_NT), 0, (hipStream_t)stream, tk, tv, H, D,
+                               move, keep);
         return ma_check_launch(who);
     }
     return MA_OK;

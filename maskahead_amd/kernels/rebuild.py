@@ -46,6 +46,17 @@ def rebuild_plan(phys: torch.Tensor, pos: torch.Tensor, live: int, *, quantized_
     Returns (groups_before, encode, stage) int64 [L, B, H, width], each cut to the largest
     count of any lane and padded with -1 -- the reference's ``packed`` lists.  One host
     synchronisation (the counts), as in the reference."""
+    launched = rebuild_plan_launch(phys, pos, live, quantized_length=quantized_length, need=need,
+                                   tail_groups=tail_groups, window=window)
+    return rebuild_plan_cut(launched, launched[3].cpu())
+
+
+def rebuild_plan_launch(phys: torch.Tensor, pos: torch.Tensor, live: int, *, quantized_length: int, need: int,
+                        tail_groups: int, window: int):
+    """rebuild_plan's launch alone, with no host synchronisation: (groups_before, encode,
+    stage, counts, lead) with the lists at full width and counts int32 [lanes, 3] on the
+    device.  rebuild_plan_cut finishes it from counts read back by the caller -- one read
+    for the plans of several caches."""
     N.require_gpu(phys, "phys")
     if phys.dtype != torch.int32:
         raise ValueError("phys must be int32")
@@ -65,18 +76,26 @@ def rebuild_plan(phys: torch.Tensor, pos: torch.Tensor, live: int, *, quantized_
     enc = torch.empty((lanes, max(live, 1)), device=dev, dtype=torch.int64)
     stg = torch.empty((lanes, max(live, 1)), device=dev, dtype=torch.int64)
     counts = torch.empty((lanes, 3), device=dev, dtype=torch.int32)
-    if lanes == 0:
-        empty = torch.empty((*lead, 0), device=dev, dtype=torch.int64)
+    if lanes:
+        N.call("ma_rebuild_plan", p2.data_ptr(), p2.stride(0), q2.data_ptr(), int(pos.dtype == torch.int64),
+               q2.stride(0), lanes, int(live), int(quantized_length), int(need), int(tail_groups), int(window),
+               gb.data_ptr(), gb.stride(0), enc.data_ptr(), enc.stride(0), stg.data_ptr(), stg.stride(0),
+               counts.data_ptr(), N.stream_of(phys))
+    return gb, enc, stg, counts, lead
+
+
+def rebuild_plan_cut(launched, counts_host: torch.Tensor):
+    """The lists of a rebuild_plan_launch, cut to the largest count of any lane; counts_host
+    is its counts tensor read back to the host."""
+    gb, enc, stg, _, lead = launched
+    c = counts_host.reshape(-1, 3)
+    if c.shape[0] == 0:
+        empty = torch.empty((*lead, 0), device=gb.device, dtype=torch.int64)
         return empty, empty, empty
-    N.call("ma_rebuild_plan", p2.data_ptr(), p2.stride(0), q2.data_ptr(), int(pos.dtype == torch.int64),
-           q2.stride(0), lanes, int(live), int(quantized_length), int(need), int(tail_groups), int(window),
-           gb.data_ptr(), gb.stride(0), enc.data_ptr(), enc.stride(0), stg.data_ptr(), stg.stride(0),
-           counts.data_ptr(), N.stream_of(phys))
-    c = counts.cpu()
     if bool((c < 0).any()):
         raise N.KernelUnavailableError("rebuild plan: a lane holds more than 16384 live entries out of position "
                                        "order; only ordered lanes of that size are built")
-    g1, m, st = (int(x) for x in c.max(0).values) if lanes else (0, 0, 0)
+    g1, m, st = (int(x) for x in c.max(0).values)
     return (gb[:, :g1].reshape(*lead, g1), enc[:, :m].reshape(*lead, m), stg[:, :st].reshape(*lead, st))
 
 

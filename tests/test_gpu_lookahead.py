@@ -131,6 +131,14 @@ def test_lookahead_probe_evict_then_masked_attention(gpu):
         a = (a1b[layer] + fp.probe_mass[layer]).cpu()
         gi = new_phys[layer].unsqueeze(-1).expand(-1, -1, -1, d)
         assert torch.equal(score2[layer].cpu(), OA.value_score_bf16(a, vd2[layer].gather(2, gi)))
+    # the same from masses kept per physical slot (step 0 without live_slots), put in live
+    # order by lookahead_scores for all layers at once
+    a1_slot = {}
+    for layer in range(L):
+        fp.step0(layer, q3.to(gpu), k3.to(gpu), v3.to(gpu), select=False, topk=1, want_mass=True)
+        a1_slot[layer] = fp.last_mass[layer]
+        assert a1_slot[layer].shape == (1, hkv, cache.length)
+    assert torch.equal(lookahead_scores(cache, st, a1_slot, fp.probe_mass, use_value=True, per_slot=True), score2)
     C2 = 768
     pos1 = st.pos[..., :live].cpu().to(torch.int64)
     # the decode loop's hot path: no order-check or rebuild-status read-back
@@ -139,3 +147,52 @@ def test_lookahead_probe_evict_then_masked_attention(gpu):
     assert torch.equal(keep2.cpu(), OS.keep_select(pos1, score2.cpu(), C2, W))
     assert st.live == C2
     cache.check_rebuild()
+
+
+def test_lookahead_evict_batch_equals_one_by_one(gpu):
+    """lookahead_evict_batch over the sequences of a batch (each with its own cache and
+    state; the plans' counts read back once for all of them) leaves every cache, state
+    and keep set exactly as lookahead_evict called on each sequence in turn does; a
+    sequence whose live set already fits is left alone."""
+    from maskahead_amd.runtime.session import lookahead_evict_batch
+
+    L, hkv, d, t, C, W = 2, 4, 128, 32, 512, 64
+    cfg = EvictionConfig(policy="lookahead", recent_window=W, capacity_floor=W, compaction="lazy", repack_below=0.5)
+
+    def build(n, seed):
+        q, k, v, kc, vc = layer_inputs(b=1, hq=28, hkv=hkv, d=d, n=n, t=t, seed=seed)
+        cache = PackedKVCache(num_layers=L, batch_size=1, num_kv_heads=hkv, head_dim=d, max_tokens=1 << 14,
+                              quant=QuantizationConfig(), device=gpu)
+        cache.begin_append(n)
+        for layer in range(L):
+            cache.stage_layer(layer, (k + layer).to(torch.bfloat16).to(gpu), v.to(torch.bfloat16).to(gpu))
+        cache.commit_append()
+        st = EvictionState(num_layers=L, batch_size=1, num_kv_heads=hkv, capacity=n, device=gpu)
+        st.append(range(n))
+        fp = FastLayerPath(cache=cache, block_size=t, query_indices=list(range(t)))
+        for layer in range(L):
+            fp.step0(layer, q.to(torch.bfloat16).to(gpu), kc.to(torch.bfloat16).to(gpu),
+                     vc.to(torch.bfloat16).to(gpu), select=False, topk=1, want_mass=True)
+        return cache, st, dict(fp.last_mass)
+
+    lens = (2000, 3100, 400)                    # the last one already fits the capacity
+    one = [build(n, 80 + i) for i, n in enumerate(lens)]
+    many = [build(n, 80 + i) for i, n in enumerate(lens)]
+    keeps1 = [lookahead_evict(c, s, cfg, C, a1, None, next_position=n, check=False)
+              for (c, s, a1), n in zip(one, lens)]
+    keeps2 = lookahead_evict_batch([(c, s, a1, None, n) for (c, s, a1), n in zip(many, lens)], cfg, C)
+    torch.cuda.synchronize()
+    assert keeps1[2] is None and keeps2[2] is None
+    for (c1, s1, _), (c2, s2, _), k1, k2 in zip(one, many, keeps1, keeps2):
+        c1.check_rebuild()
+        c2.check_rebuild()
+        assert (k1 is None) == (k2 is None) and (k1 is None or torch.equal(k1, k2))
+        assert (c1.length, c1.quantized_length, c1.residual_length, c1.dropped) == \
+            (c2.length, c2.quantized_length, c2.residual_length, c2.dropped)
+        assert s1.live == s2.live and torch.equal(s1.phys[..., :s1.live], s2.phys[..., :s2.live])
+        assert torch.equal(s1.pos[..., :s1.live], s2.pos[..., :s2.live])
+        for _, name in STORE:
+            a, b = getattr(c1, name), getattr(c2, name)
+            cut = c1.quantized_length // 32 if name in ("k_q", "k_scale", "k_zero") else \
+                c1.quantized_length if name.startswith("v_") and name != "v_residual" else c1.residual_length
+            assert same_bits(a[:, :, :, :cut], b[:, :, :, :cut]), name
