@@ -184,6 +184,160 @@ __global__ void __launch_bounds__(VS_NT) vs_partial_kernel(VsArgs a) {
     }
 }
 
+// The all-bf16 form of the two passes (rows, 16-bit cache rows and vdtype bf16; bf16
+// mode): the same arithmetic as vs_partial_kernel / vs_score_kernel with every load of a
+// batch of VS_BATCH steps issued as straight-line code -- the slots (or rows) first, then
+// the codes, scales and 16-bit rows they name, at clamped addresses, the choices made by
+// selects afterwards -- so a thread has a batch's loads in flight together instead of
+// waiting for them one branch at a time.  HASQ / HASF: the cache lane has packed slots /
+// 16-bit rows (slot form; the dense form reads rows).
+template <bool SLOTS, bool HASQ, bool HASF>
+__device__ __forceinline__ void load_batch_bf(const VsArgs &a, int row, int jb, int j0, int j1, int tl, int c0,
+                                              float (&x)[VS_BATCH][8], float (&aw)[VS_BATCH]) {
+    const float *ar = a.a + (int64_t)row * a.sa;
+    int jl[VS_BATCH];
+#pragma unroll
+    for (int u = 0; u < VS_BATCH; ++u) {
+        const int j = jb + u * VS_TOK + tl;
+        jl[u] = j < j1 ? j : j0;
+        aw[u] = ar[jl[u]];
+    }
+    if constexpr (!SLOTS) {
+        uint4 w[VS_BATCH];
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) w[u] = *(const uint4 *)((const uint16_t *)vrow(a, row, jl[u]) + c0);
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const uint32_t wv[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[u][i] = ma_bf16_to_f32((uint16_t)(wv[i >> 1] >> ((i & 1) * 16)));
+        }
+    } else {
+        const int b = row / a.H, h = row % a.H;
+        int sl[VS_BATCH];
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) sl[u] = a.slots[(int64_t)row * a.sslot + jl[u]];
+        const int cg = c0 / 32;
+        uint32_t w[VS_BATCH];
+        uint16_t scb[VS_BATCH], zeb[VS_BATCH];
+        uint4 r[VS_BATCH];
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const int s = sl[u];
+            if constexpr (HASQ) {
+                const int sq = s >= 0 && s < a.nq ? s : 0;
+                w[u] = *(const uint32_t *)(a.vq + b * a.svq[0] + h * a.svq[1] + (int64_t)sq * a.svq[2] +
+                                           cg * a.svq[3] + (c0 % 32) / 2);
+                const int64_t so = b * a.svs[0] + h * a.svs[1] + (int64_t)sq * a.svs[2] + cg;
+                scb[u] = a.vsc[so];
+                zeb[u] = a.vzp[so];
+            }
+            if constexpr (HASF) {
+                const int sf = s >= a.nq && s < a.nq + a.nf ? s - a.nq : 0;
+                r[u] = *(const uint4 *)((const uint16_t *)a.vf + b * a.svf[0] + h * a.svf[1] +
+                                        (int64_t)sf * a.svf[2] + c0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const int s = sl[u];
+            const bool q = HASQ && s >= 0 && s < a.nq, f = HASF && s >= a.nq && s < a.nq + a.nf;
+            float sc = 0.f, ze = 0.f;
+            uint32_t wu = 0;
+            uint32_t rv[4] = {0u, 0u, 0u, 0u};
+            if constexpr (HASQ) {
+                sc = ma_f16_to_f32(scb[u]);
+                ze = ma_f16_to_f32(zeb[u]);
+                wu = w[u];
+            }
+            if constexpr (HASF) {
+                rv[0] = r[u].x;
+                rv[1] = r[u].y;
+                rv[2] = r[u].z;
+                rv[3] = r[u].w;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float xq = ma_round_bf16(ma_dq((wu >> (4 * i)) & 15u, sc, ze));
+                const float xf = ma_bf16_to_f32((uint16_t)(rv[i >> 1] >> ((i & 1) * 16)));
+                x[u][i] = q ? xq : (f ? xf : 0.f);
+            }
+        }
+    }
+}
+
+template <bool SLOTS, bool HASQ, bool HASF>
+__global__ void __launch_bounds__(VS_NT) vs_partial_bf_kernel(VsArgs a) {
+    __shared__ double red[VS_TOK][129];
+    const int chunk = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int tl = tid / 16, oc = tid % 16;
+    const bool cok = oc * 8 < a.D;
+    const int c0 = cok ? oc * 8 : 0;        // lanes past D read channel 0 and are not written
+    const int j0 = chunk * a.chunk, j1 = min(j0 + a.chunk, a.n);
+    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    double den = 0.0;
+    for (int jb = j0; jb < j1; jb += VS_TOK * VS_BATCH) {
+        float aw[VS_BATCH], x[VS_BATCH][8];
+        load_batch_bf<SLOTS, HASQ, HASF>(a, row, jb, j0, j1, tl, c0, x, aw);
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const bool ok = jb + u * VS_TOK + tl < j1;
+            const double w = ok ? (double)ma_round_bf16(aw[u]) : 0.0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = __builtin_fma(w, (double)x[u][i], acc[i]);
+            den += w;
+        }
+    }
+    if (cok)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) red[tl][c0 + i] = acc[i];
+    if (oc == 0) red[tl][128] = den;
+    __syncthreads();
+    double *out = a.part + ((int64_t)row * a.nchunks + chunk) * (a.D + 1);
+    for (int c = tid; c <= a.D; c += VS_NT) {
+        const int cc = c == a.D ? 128 : c;
+        double s = 0.0;
+#pragma unroll
+        for (int t = 0; t < VS_TOK; ++t) s += red[t][cc];
+        out[c] = s;
+    }
+}
+
+template <bool SLOTS, bool HASQ, bool HASF>
+__global__ void __launch_bounds__(VS_NT) vs_score_bf_kernel(VsArgs a) {
+    __shared__ float cen[128];
+    const int chunk = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    for (int d = tid; d < a.D; d += VS_NT) cen[d] = a.centre[(int64_t)row * a.D + d];
+    __syncthreads();
+    const int tl = tid / 16, oc = tid % 16;
+    const bool cok = oc * 8 < a.D;
+    const int c0 = cok ? oc * 8 : 0;
+    const int j0 = chunk * a.chunk, j1 = min(j0 + a.chunk, a.n);
+    float *sr = a.score + (int64_t)row * a.ss;
+    float cc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cc[i] = cen[c0 + i];
+    for (int jb0 = j0; jb0 < j1; jb0 += VS_TOK * VS_BATCH) {
+        float x[VS_BATCH][8], aw[VS_BATCH];
+        load_batch_bf<SLOTS, HASQ, HASF>(a, row, jb0, j0, j1, tl, c0, x, aw);
+#pragma unroll
+        for (int u = 0; u < VS_BATCH; ++u) {
+            const int j = jb0 + u * VS_TOK + tl;
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float dl = ma_round_bf16(x[u][i] - cc[i]);
+                ss = __builtin_fma((double)dl, (double)dl, ss);
+            }
+            if (!cok) ss = 0.0;
+            // sum over the 16 lanes of this entry (lanes tl*16 .. tl*16+15 of the wave pair)
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+            if (j < j1 && oc == 0) sr[j] = aw[u] * bf16_via_f32(__builtin_sqrt(ss));
+        }
+    }
+}
+
 // grid rows, VC_NT threads: centre[row, d] from the chunk partials.  Thread (slot s,
 // column d) sums the chunks s, s + VC_SLOTS, ... (VC_UNROLL loads in flight), then the
 // slots are added in slot order: a fixed order, and in the bf16 mode every sum of the
@@ -428,6 +582,12 @@ extern "C" int ma_value_score(const float *a, int64_t a_stride, ma_tensor4 v, in
     va.slots = nullptr;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid(va.nchunks, rows);
+    if (v.dtype == MA_BF16 && !fp32_mode) {
+        hipLaunchKernelGGL((vs_partial_bf_kernel<false, false, false>), grid, dim3(VS_NT), 0, st, va);
+        hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
+        hipLaunchKernelGGL((vs_score_bf_kernel<false, false, false>), grid, dim3(VS_NT), 0, st, va);
+        return ma_check_launch(who);
+    }
     hipLaunchKernelGGL(vs_partial_kernel<false>, grid, dim3(VS_NT), 0, st, va);
     hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
     hipLaunchKernelGGL(vs_score_kernel<false>, grid, dim3(VS_NT), 0, st, va);
@@ -494,6 +654,18 @@ extern "C" int ma_value_score_slots(const float *a, int64_t a_stride, const ma_p
     va.fdtype = p->fdtype;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid(va.nchunks, rows);
+    if (vdtype == MA_BF16 && !fp32_mode && (p->nf == 0 || p->fdtype == MA_BF16)) {
+        // the all-bf16 passes, instantiated for packed slots, 16-bit rows or both
+        auto both = [&](auto partial, auto score) {
+            hipLaunchKernelGGL(partial, grid, dim3(VS_NT), 0, st, va);
+            hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
+            hipLaunchKernelGGL(score, grid, dim3(VS_NT), 0, st, va);
+        };
+        if (p->nq > 0 && p->nf > 0) both(vs_partial_bf_kernel<true, true, true>, vs_score_bf_kernel<true, true, true>);
+        else if (p->nq > 0) both(vs_partial_bf_kernel<true, true, false>, vs_score_bf_kernel<true, true, false>);
+        else both(vs_partial_bf_kernel<true, false, true>, vs_score_bf_kernel<true, false, true>);
+        return ma_check_launch(who);
+    }
     hipLaunchKernelGGL(vs_partial_kernel<true>, grid, dim3(VS_NT), 0, st, va);
     hipLaunchKernelGGL(vs_centre_kernel, dim3(rows), dim3(VC_NT), 0, st, va);
     hipLaunchKernelGGL(vs_score_kernel<true>, grid, dim3(VS_NT), 0, st, va);
