@@ -414,13 +414,18 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
     const int nt = (n_end - n_beg + TILE - 1) / TILE;
     const int slot = wk.cur ? a.nsplit : a.slot0 + wk.sp;
     DSrc ds;
-    if constexpr (SRC == 1) {
+    if constexpr (SRC != 0) {
         if (wk.cur) {
             const Dense kc = dense_lane(a.kc.ptr, a.kc.s, a.kc.dtype, b, h);
             const Dense vc = dense_lane(a.vc.ptr, a.vc.s, a.vc.dtype, b, h);
             ds = DSrc{kc.base, vc.base, kc.sn, vc.sn, kc.dtype, kc.esz, 0, nullptr};
         } else {
             ds = DSrc{L.kf, L.vf, L.kf_n, L.vf_n, L.fdtype, L.esz, L.nq, L.mask};
+        }
+        if constexpr (SRC == 2) {
+            // every 16-bit operand of the launch is bf16: the staging's dtype choices fold
+            ds.dtype = MA_BF16;
+            ds.esz = 2;
         }
     }
 
@@ -912,7 +917,12 @@ int launch_partial_d(const Plan &pl, hipStream_t st) {
         fa.tok_beg = nq;
         fa.tok_end = nq + nf;
         fa.with_cur = 1;
-        hipLaunchKernelGGL((splitk_fwd_kernel<D, 1, false>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
+        const bool bf = (nf == 0 || fa.pre.fdtype == MA_BF16) &&
+                        (fa.Tc == 0 || (fa.kc.dtype == MA_BF16 && fa.vc.dtype == MA_BF16));
+        if (bf)
+            hipLaunchKernelGGL((splitk_fwd_kernel<D, 2, false>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
+        else
+            hipLaunchKernelGGL((splitk_fwd_kernel<D, 1, false>), dim3((nsf + 1) * units), dim3(NTH), 0, st, fa);
     }
     return ma_check_launch("ma_splitk_partial");
 }
