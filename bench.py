@@ -404,7 +404,7 @@ def bench_substep(a):
                    "split_tokens": a.split_tokens or "auto", "algorithmic_bytes": nbytes, "algorithmic_flops": flops},
         "roofline": {"bound": "hbm" if nbytes / HBM_PEAK_GBS / 1e9 >= flops / MFMA_BF16_PEAK_TFLOPS / 1e12 else "mfma",
                      "achieved": round(nbytes / t / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(f_hbm, 4), "traffic": None, "kernel": "splitk_fwd_kernel<128, 1> + "
+                     "frac": round(f_hbm, 4), "traffic": None, "kernel": "splitk_fwd_kernel<128, 2> + "
                      "splitk_combine_kernel<128> (whole sub-step)", "avg_launch_us": round(us, 3),
                      "mfma_frac": round(f_mfma, 4)},
     }

@@ -161,7 +161,9 @@ def dtype_code(dt: torch.dtype) -> int:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The raw handle of the current stream of t's device (what torch's own kernels are
+    launched on), without building a torch.cuda.Stream object."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

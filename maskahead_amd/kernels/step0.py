@@ -80,7 +80,7 @@ def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, curren
     rows_key = rows if isinstance(rows, torch.Tensor) else tuple(rows)
     views = tuple(None if x is None else (x.data_ptr(), x.shape, x.stride(), x.dtype) for x in (out_key, out_value))
     key = (query.shape, query.stride(), query.dtype, current_key.shape, current_key.stride(), current_value.stride(),
-           current_key.dtype, int(k), bool(value), scaling, views, stream)
+           current_key.dtype, current_value.dtype, int(k), bool(value), scaling, views, stream)
     plan = bufs._plan
     # (prefix.native() returns the same descriptor object while the prefix's tensors and
     # mask are the ones it was built from)
@@ -88,10 +88,10 @@ def step0_select(bufs: Step0Buffers, query: torch.Tensor, prefix: Prefix, curren
             and (plan[3] is rows_key if isinstance(rows_key, torch.Tensor) else plan[3] == rows_key)
             and plan[4][5] is prefix.native()):
         args, result = plan[4], plan[5]
-        tc = current_key.shape[2]
-        args[0] = N.t4(query)
-        args[7] = N.t4(current_key if tc else None)
-        args[8] = N.t4(current_value if tc else None)
+        # the same shapes, strides and dtypes (the key): only the operands' addresses change
+        args[0].ptr = query.data_ptr()
+        if current_key.shape[2]:
+            args[7].ptr, args[8].ptr = current_key.data_ptr(), current_value.data_ptr()
         N.check(N.load().ma_step0(*args), "ma_step0")
         return result
     if query.ndim != 4 or current_key.ndim != 4:

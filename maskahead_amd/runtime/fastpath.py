@@ -293,8 +293,10 @@ class FastLayerPath:
             # with this call's operands and a fresh output
             args = hit[2]
             out = torch.empty_like(q)
-            tc = kc.shape[2]
-            args[0], args[7], args[8], args[14] = N.t4(q), N.t4(kc if tc else None), N.t4(vc if tc else None), N.t4(out)
+            # the same shapes, strides and dtypes: only the operands' addresses change
+            args[0].ptr, args[14].ptr = q.data_ptr(), out.data_ptr()
+            if ncur:
+                args[7].ptr, args[8].ptr = kc.data_ptr(), vc.data_ptr()
             N.check(N.load().ma_splitk_attention(*args), "ma_splitk_attention")
             return out.to(query.dtype)
         pre = Prefix.dense(state.key[:, :, :k, :], state.value[:, :, :k, :])
