@@ -140,6 +140,7 @@ class PackedKVCache:
         # of views or descriptors of the planes drop them when it changes
         self.planes_generation = 0
         self._pending_rebuild_status: torch.Tensor | None = None   # a rebuild's unread errors
+        self._append_geo: tuple | None = None     # ma_append_packed's plane geometry (_append_packed)
         for name in _UNITS:
             setattr(self, name, None)
         gk = quant.key_token_group
@@ -315,19 +316,39 @@ class PackedKVCache:
                 and value.stride(-1) == 1 and q.k_bits == 4 and q.v_bits == 4 and q.key_token_group == 32
                 and q.value_channel_group == 32 and self.k_fp is None and self.v_fp is None)
 
+    _APPEND_PLANES = ("k_q", "k_scale", "k_zero", "v_q", "v_scale", "v_zero", "k_residual", "v_residual")
+
     def _append_packed(self, layer_idx: int, plan: "AppendPlan", key: torch.Tensor, value: torch.Tensor) -> None:
         """One layer's packed append in one ma_append_packed call: the whole key groups of
         [residual | new] quantized into the planes after the quantized part, the rest left
-        as the residual (the same bytes as the quantizers over the concatenated tail)."""
+        as the residual (the same bytes as the quantizers over the concatenated tail).  The
+        planes' strides and element sizes are kept while the planes are the same storage,
+        so a call computes only its addresses."""
         move, keep = plan.quantize_from_residual, plan.new_residual
+        planes = [getattr(self, name) for name in self._APPEND_PLANES]
+        # every replacement of the planes bumps planes_generation (a new plane may reuse a
+        # freed one's address with other strides)
+        ptrs = (self.planes_generation,) + tuple(t.data_ptr() for t in planes)
+        geo = self._append_geo
+        if geo is None or geo[0] != ptrs:
+            # per plane: (base address, bytes per layer, bytes per row unit) and the strides of
+            # a layer's view; the residual planes as ma_tensor4 templates
+            lay = [(t.data_ptr(), t.stride(0) * t.element_size(), t.stride(3) * t.element_size()) for t in planes]
+            arrs = [N.i64arr(*t.stride()[1:5]) for t in planes[0:1]] + [N.i64arr(*planes[1].stride()[1:4])] + \
+                [N.i64arr(*planes[3].stride()[1:5])] + [N.i64arr(*planes[4].stride()[1:4])]
+            kres, vres = N.t4(planes[6][0]), N.t4(planes[7][0])
+            geo = self._append_geo = (ptrs, lay, arrs, kres, vres)
+        _, lay, arrs, kres, vres = geo
         g0, t0 = self.quantized_length // self.quant.key_token_group, self.quantized_length
-        kq, ks, kz = (x[layer_idx, :, :, g0:] for x in (self.k_q, self.k_scale, self.k_zero))
-        vq, vs, vz = (x[layer_idx, :, :, t0:] for x in (self.v_q, self.v_scale, self.v_zero))
+
+        def at(i, row):
+            base, per_layer, per_row = lay[i]
+            return base + layer_idx * per_layer + row * per_row
+
+        kres.ptr, vres.ptr = at(6, 0), at(7, 0)
         b, h, t, d = key.shape
-        N.call("ma_append_packed", N.t4(self.k_residual[layer_idx]), N.t4(self.v_residual[layer_idx]),
-               plan.old_residual, N.t4(key), N.t4(value), b, h, t, d, move, keep, kq.data_ptr(),
-               N.i64arr(*kq.stride()[:4]), ks.data_ptr(), kz.data_ptr(), N.i64arr(*ks.stride()[:3]), vq.data_ptr(),
-               N.i64arr(*vq.stride()[:4]), vs.data_ptr(), vz.data_ptr(), N.i64arr(*vs.stride()[:3]),
+        N.call("ma_append_packed", kres, vres, plan.old_residual, N.t4(key), N.t4(value), b, h, t, d, move, keep,
+               at(0, g0), arrs[0], at(1, g0), at(2, g0), arrs[1], at(3, t0), arrs[2], at(4, t0), at(5, t0), arrs[3],
                N.stream_of(key))
 
     def _tail(self, residual: torch.Tensor, old: int, new: torch.Tensor) -> torch.Tensor:

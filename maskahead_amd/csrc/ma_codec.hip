@@ -285,7 +285,7 @@ __global__ void __launch_bounds__(RK_NT) residual_keep_kernel(TwoSrc k, TwoSrc v
     const int first = move == 0 ? s.na : 0;      // move = 0: a's rows stay, b's follow them
     const int per = RK_NT / D;                   // rows per pass of the workgroup
     const int r0 = threadIdx.x / D, d = threadIdx.x % D;
-    constexpr int RPT = 8;                       // rows per thread per chunk
+    constexpr int RPT = 32;                      // rows per thread per chunk (64 rows at D = 128)
     char *dst = (char *)s.a.ptr;
     for (int c0 = first; c0 < keep; c0 += per * RPT) {
         float x[RPT];
