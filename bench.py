@@ -769,12 +769,11 @@ def extra_c4_block(a, L=28, dense=2):
     scores with the fused read-set select, gather), the lookahead eviction (keep score,
     keep set, packed lazy rebuild), 3 denoising sub-steps and the block's finalize (its KV
     appended) (session.py:1403-1454, 1985-2034, 270-361, 1286-1336, 2289-2297).  Launched
-    op by op from Python as the session runs it, phase by phase as a batched forward does
-    (each layer's calls for every sequence in turn), so the host's launches of one
-    sequence overlap the GPU work of the others; the evictions of the batch read their
-    plans' counts back in one synchronisation (lookahead_evict_batch).
-    Algorithmic
-    bytes per sequence of prefix n (P = n x 4 KV heads x 160 B of int4 K and V with their
+    op by op from Python, phase by phase as a batched forward does (BatchFastPath: each
+    layer's step 0 per sequence over its own prefix, its sub-steps as one call over the
+    batch's shared compact buffer), so the host's launches of one sequence overlap the GPU
+    work of the others; the evictions of the batch read their plans' counts back in one
+    synchronisation (lookahead_evict_batch).  Algorithmic bytes per sequence of prefix n (P = n x 4 KV heads x 160 B of int4 K and V with their
     scales): step 0 streams the prefix twice in a sparse layer (attention, scores) and once
     in a dense one; the eviction reads V once per layer (keep score) and reads and writes
     the 4 096 kept entries; the sub-steps read the 2 048-entry bf16 compact buffers of the
@@ -782,7 +781,8 @@ def extra_c4_block(a, L=28, dense=2):
     from maskahead_amd.cache import PackedKVCache
     from maskahead_amd.config import QuantizationConfig
     from maskahead_amd.eviction import EvictionConfig, EvictionState
-    from maskahead_amd.runtime.fastpath import BlockContext, FastLayerPath
+    from maskahead_amd.runtime.batch import BatchFastPath
+    from maskahead_amd.runtime.fastpath import BlockContext
     from maskahead_amd.runtime.session import live_slot_masks, lookahead_evict_batch
 
     dev = torch.device("cuda:0")
@@ -792,7 +792,7 @@ def extra_c4_block(a, L=28, dense=2):
                          repack_below=1.0, sink_tokens=4)
 
     class Seq:
-        """One sequence of the batch: its cache, eviction state, fast path and block inputs."""
+        """One sequence of the batch: its cache, eviction state and block inputs."""
 
         def __init__(self, n, seed):
             g = torch.Generator(device=dev).manual_seed(seed)
@@ -814,37 +814,48 @@ def extra_c4_block(a, L=28, dense=2):
             del k, v
             self.st = EvictionState(num_layers=L, batch_size=1, num_kv_heads=hkv, capacity=n + 4 * t, device=dev)
             self.st.append(range(n))
-            self.fp = FastLayerPath(cache=self.cache, block_size=t, query_indices=list(range(t)),
-                                    dense_prefix_layers=dense)
             self.n = n
 
-    def block_step(seqs):
+    class Batch:
+        """The batch as a batched forward hands it over: every layer's block queries and K/V
+        as [8, H, 32, D] tensors, and one BatchFastPath over the 8 caches (one compact
+        buffer [8, Hkv, 2048 + 32, D] per layer, as the reference's batched session keeps)."""
+
+        def __init__(self, seqs):
+            self.seqs = seqs
+            self.blocks = [tuple(torch.cat([s.blocks[layer][j] for s in seqs]) for j in range(3)) for layer in range(L)]
+            for s in seqs:
+                del s.blocks
+            self.bp = BatchFastPath([s.cache for s in seqs], block_size=t, query_indices=list(range(t)),
+                                    dense_prefix_layers=dense)
+
+    def block_step(batch):
         """One block of the batch, phase by phase as a batched forward runs it: step 0 of
-        every layer (layer by layer, every sequence in turn), the lookahead eviction of every
-        sequence, 3 sub-steps (likewise), the finalize.  Returns the seconds it took."""
+        every layer (each sequence over its own prefix), the lookahead eviction of every
+        sequence, 3 sub-steps (one call per sparse layer over the batch's compact buffer),
+        the finalize.  Returns the seconds it took."""
+        seqs, bp, blocks = batch.seqs, batch.bp, batch.blocks
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for s in seqs:
-            # step 0 keeps each layer's mass per physical slot; the eviction puts all layers'
-            # in live order at once (lookahead_scores, per_slot)
-            s.ctx = BlockContext(step_index=0, old_cache_len=s.n, topk=read_k, evicting=True, live_len=s.st.live,
-                                 want_mass=True)
+        # step 0 keeps each layer's mass per physical slot; the eviction puts all layers' in
+        # live order at once (lookahead_scores, per_slot)
+        ctxs = [BlockContext(step_index=0, old_cache_len=s.n, topk=read_k, evicting=True, live_len=s.st.live,
+                             want_mass=True) for s in seqs]
         for layer in range(L):
-            for s in seqs:
-                s.fp.route(layer, *s.blocks[layer], s.ctx)
-        lookahead_evict_batch([(s.cache, s.st, s.fp.last_mass, None, s.n) for s in seqs], cfg, keep_k, per_slot=True)
-        for s in seqs:
-            s.fp.slot_masks = live_slot_masks(s.cache, s.st)
+            bp.route(layer, *blocks[layer], ctxs)
+        lookahead_evict_batch([(s.cache, s.st, p.last_mass, None, s.n) for s, p in zip(seqs, bp.paths)], cfg, keep_k,
+                              per_slot=True)
+        for s, p in zip(seqs, bp.paths):
+            p.slot_masks = live_slot_masks(s.cache, s.st)
         for step in (1, 2, 3):
-            for s in seqs:
-                s.ctx.step_index = step
+            for ctx in ctxs:
+                ctx.step_index = step
             for layer in range(L):
-                for s in seqs:
-                    s.fp.route(layer, *s.blocks[layer], s.ctx)
-        for s in seqs:
+                bp.route(layer, *blocks[layer], ctxs)
+        for i, s in enumerate(seqs):
             s.cache.begin_append(t)
             for layer in range(L):
-                s.cache.stage_layer(layer, s.blocks[layer][1], s.blocks[layer][2])
+                s.cache.stage_layer(layer, blocks[layer][1][i:i + 1], blocks[layer][2][i:i + 1])
             s.cache.commit_append()
             s.st.append(range(s.n, s.n + t))
         torch.cuda.synchronize()
@@ -856,12 +867,12 @@ def extra_c4_block(a, L=28, dense=2):
     # warm-up: the same batch once (kernels loaded, and torch's caching allocator grown to
     # the batch's footprint, so the timed block reuses its blocks as a serving process does:
     # a cold allocator's device allocations synchronize the host); then fresh caches
-    seqs = [Seq(n, 1234 + i) for i, n in enumerate(lens)]
-    block_step(seqs)
-    del seqs
-    seqs = [Seq(n, 1234 + i) for i, n in enumerate(lens)]
-    sec = block_step(seqs)
-    del seqs
+    batch = Batch([Seq(n, 1234 + i) for i, n in enumerate(lens)])
+    block_step(batch)
+    del batch
+    batch = Batch([Seq(n, 1234 + i) for i, n in enumerate(lens)])
+    sec = block_step(batch)
+    del batch
     torch.cuda.empty_cache()
     r = (hq // hkv) * t
     nbytes = flops = 0
@@ -874,7 +885,8 @@ def extra_c4_block(a, L=28, dense=2):
         flops += 3 * ((L - dense) * 4 * r * read_k * d * hkv + dense * 4 * r * keep_k * d * hkv)
     return {"workload": f"c4: 8 sequences, prefixes {sorted(lens)}, 28 layers ({dense} dense), packed int4, "
                         f"read {read_k} / keep {keep_k}: one block of the batch -- step 0 of every layer, the "
-                        f"lookahead eviction, 3 sub-steps, the finalize -- eager, phase by phase over the sequences",
+                        f"lookahead eviction, 3 sub-steps, the finalize -- eager, phase by phase; sub-steps batched "
+                        f"over the sequences (BatchFastPath)",
             "us_per_block_step": round(sec * 1e6, 1), "roofline": _roof(nbytes, flops, sec)}
 
 

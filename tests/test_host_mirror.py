@@ -146,3 +146,21 @@ def test_bind_session_host():
     from maskahead_amd.runtime.session import value_score
 
     assert mod.value_score is value_score and old is not value_score
+
+
+def test_batch_fast_path_checks_its_caches():
+    """BatchFastPath takes one single-sequence cache per sequence, all of one head shape."""
+    from maskahead_amd.runtime.batch import BatchFastPath
+
+    def cache(d=128, b=1):
+        return PackedKVCache(num_layers=2, batch_size=b, num_kv_heads=4, head_dim=d, max_tokens=256,
+                             quant=QuantizationConfig(), device="cpu")
+
+    with pytest.raises(ValueError):
+        BatchFastPath([], block_size=32)
+    with pytest.raises(ValueError):
+        BatchFastPath([cache(), cache(d=64)], block_size=32)
+    with pytest.raises(ValueError):
+        BatchFastPath([cache(b=2)], block_size=32)
+    bp = BatchFastPath([cache(), cache()], block_size=32, query_indices=range(32), dense_prefix_layers=1)
+    assert bp.batch_size == 2 and all(p.dense_prefix_layers == 1 for p in bp.paths)
