@@ -783,7 +783,7 @@ def extra_c4_block(a, L=28, dense=2):
     from maskahead_amd.eviction import EvictionConfig, EvictionState
     from maskahead_amd.runtime.batch import BatchFastPath
     from maskahead_amd.runtime.fastpath import BlockContext
-    from maskahead_amd.runtime.session import live_slot_masks, lookahead_evict_batch
+    from maskahead_amd.runtime.session import admit_new_entries, live_slot_masks, lookahead_evict_batch
 
     dev = torch.device("cuda:0")
     hq, hkv, d, t, read_k, keep_k, W = 28, 4, 128, 32, 2048, 4096, 64
@@ -857,7 +857,7 @@ def extra_c4_block(a, L=28, dense=2):
             for layer in range(L):
                 s.cache.stage_layer(layer, blocks[layer][1][i:i + 1], blocks[layer][2][i:i + 1])
             s.cache.commit_append()
-            s.st.append(range(s.n, s.n + t))
+            admit_new_entries(s.cache, s.st, s.n)
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
         for s in seqs:

@@ -128,11 +128,32 @@ def live_slot_masks(cache, state) -> dict:
     live = state.live
     if cache.length <= live:
         return {}
+    phys = state.phys[..., :live].to(torch.int64)
+    # the scatter below does not check its indices on the GPU: a slot outside the cache
+    # (entries admitted with their positions as slots after a compaction, instead of
+    # admit_new_entries) would write out of bounds -- refuse it here (one read-back)
+    lo, hi = torch.stack(torch.aminmax(phys)).tolist() if live else (0, 0)
+    if not 0 <= lo <= hi < cache.length:
+        raise ValueError(f"eviction state holds slots outside the cache's {cache.length} (admit entries "
+                         "appended after a compaction with admit_new_entries)")
     # every layer's mask in one [L, B, Hkv, length] tensor: three launches, not three per layer
     m = torch.zeros((state.num_layers, cache.batch_size, cache.num_kv_heads, cache.length), dtype=torch.uint8,
                     device=cache.device)
-    m.scatter_(-1, state.phys[..., :live].to(torch.int64), 1)
+    m.scatter_(-1, phys, 1)
     return {layer: m[layer] for layer in range(state.num_layers)}
+
+
+def admit_new_entries(cache, state, next_position: int) -> int:
+    """Give the cache positions committed since next_position a slot in the live set
+    (BitSieveSession._admit_new_entries, session.py:215-229): positions next_position ..
+    length-1, their slots the newest physical slots of the cache (after a compaction the
+    slots no longer equal the positions).  Returns the new next_position."""
+    length = cache.get_seq_length()
+    if length > next_position:
+        m = length - next_position
+        state.append(torch.arange(next_position, length, device=cache.device),
+                     phys=torch.arange(cache.length - m, cache.length, device=cache.device))
+    return max(length, next_position)
 
 
 def live_values(cache, state, layer_idx: int) -> torch.Tensor:

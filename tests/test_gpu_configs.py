@@ -25,7 +25,7 @@ from maskahead_amd.config import QuantizationConfig
 from maskahead_amd.eviction import EvictionConfig, EvictionState
 from maskahead_amd.kernels.splitk import prefix_scores, splitk_attention
 from maskahead_amd.runtime.fastpath import BlockContext, FastLayerPath
-from maskahead_amd.runtime.session import live_slot_masks, lookahead_evict, lookahead_scores
+from maskahead_amd.runtime.session import admit_new_entries, live_slot_masks, lookahead_evict, lookahead_scores
 from maskahead_amd.workloads import CONFIGS, layer_inputs
 from oracle import attention as OA
 from oracle import rebuild as OR
@@ -210,7 +210,10 @@ def test_config4_ragged_block_step(gpu):
         for layer in range(L):
             cache.stage_layer(layer, blocks[layer][1], blocks[layer][2])
         cache.commit_append()
-        st.append(range(n, n + t))
+        assert admit_new_entries(cache, st, n) == n + t
         assert st.live == keep_k + t and cache.get_seq_length() == n + t
+        # the admitted entries hold the newest physical slots (the cache was compacted)
+        assert torch.equal(st.phys[..., keep_k:keep_k + t].cpu(),
+                           torch.arange(cache.length - t, cache.length, dtype=torch.int32).expand(L, 1, hkv, t))
         del cache, st, fp, blocks
         torch.cuda.empty_cache()

@@ -164,3 +164,29 @@ def test_batch_fast_path_checks_its_caches():
         BatchFastPath([cache(b=2)], block_size=32)
     bp = BatchFastPath([cache(), cache()], block_size=32, query_indices=range(32), dense_prefix_layers=1)
     assert bp.batch_size == 2 and all(p.dense_prefix_layers == 1 for p in bp.paths)
+
+
+def test_admitting_entries_after_a_compaction():
+    """After a compaction the slots of newly committed entries are the cache's newest
+    physical slots, not their positions (session.py:215-229); live_slot_masks refuses a
+    state whose slots lie outside the cache instead of scattering out of bounds."""
+    from maskahead_amd.eviction import EvictionState
+    from maskahead_amd.runtime.session import admit_new_entries, live_slot_masks
+
+    cache = PackedKVCache(num_layers=2, batch_size=1, num_kv_heads=2, head_dim=128, max_tokens=4096,
+                          quant=QuantizationConfig(), device="cpu")
+    st = EvictionState(num_layers=2, batch_size=1, num_kv_heads=2, capacity=64, device="cpu")
+    # a cache that held 1000 positions, compacted to 300 physical slots, then 32 appended
+    cache.length, cache.dropped = 332, 700
+    st.append(range(250), phys=torch.arange(250) + 40)          # survivors in slots 40 .. 289
+    assert admit_new_entries(cache, st, 1000) == 1032
+    assert st.live == 282
+    assert torch.equal(st.pos[0, 0, 0, 250:282].long(), torch.arange(1000, 1032))
+    assert torch.equal(st.phys[0, 0, 0, 250:282].long(), torch.arange(300, 332))
+    masks = live_slot_masks(cache, st)
+    assert int(masks[0].sum()) == 2 * 282 and int(masks[1][0, 1, :40].sum()) == 0
+    assert admit_new_entries(cache, st, 1032) == 1032 and st.live == 282     # nothing new
+    wrong = EvictionState(num_layers=2, batch_size=1, num_kv_heads=2, capacity=64, device="cpu")
+    wrong.append(range(1000, 1032))                               # positions as slots
+    with pytest.raises(ValueError, match="outside the cache"):
+        live_slot_masks(cache, wrong)
