@@ -75,12 +75,16 @@ class BatchFastPath:
     def route(self, layer: int, query: torch.Tensor, current_key: torch.Tensor, current_value: torch.Tensor,
               ctxs) -> torch.Tensor:
         """One layer's attention for the whole batch ([B, Hq, T, D] queries, [B, Hkv, T, D]
-        block K/V; ctxs: each sequence's BlockContext), routed as FastLayerPath.route routes
+        block K/V; ctxs: each sequence's BlockContext, all in the same phase -- step index,
+        probe, prefill -- as in one batched forward), routed as FastLayerPath.route routes
         one sequence's: step 0 per sequence into the shared compact buffer, the sub-steps
         of a sparse layer in one batched call.  Returns [B, Hq, T, D]."""
         if query.shape[0] != self.batch_size or len(ctxs) != self.batch_size:
             raise ValueError(f"the batch has {self.batch_size} sequences, got {query.shape[0]} and {len(ctxs)}")
         c0 = ctxs[0]
+        phase = lambda c: (c.step_index, c.prefill, c.probe, c.qprobe_start)  # noqa: E731
+        if any(phase(c) != phase(c0) for c in ctxs):
+            raise ValueError("every sequence of a batched forward is in the same phase (step, probe, prefill)")
         if c0.prefill or c0.probe or c0.qprobe_start is not None or c0.step_index == 0:
             if c0.step_index == 0 and not (c0.prefill or c0.probe or c0.qprobe_start is not None):
                 for p, ctx in zip(self.paths, ctxs):
