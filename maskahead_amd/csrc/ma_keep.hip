@@ -256,11 +256,20 @@ __device__ __forceinline__ void load_batch_bf(const VsArgs &a, int row, int jb, 
                 rv[2] = r[u].z;
                 rv[3] = r[u].w;
             }
+            // the choice made on bf16 pairs (channels 2 i2, 2 i2 + 1 in one word, as the 16-bit
+            // rows hold them): one select and one mask per two values
+            const uint32_t keep = (q || f) ? 0xffffffffu : 0u;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float xq = ma_round_bf16(ma_dq((wu >> (4 * i)) & 15u, sc, ze));
-                const float xf = ma_bf16_to_f32((uint16_t)(rv[i >> 1] >> ((i & 1) * 16)));
-                x[u][i] = q ? xq : (f ? xf : 0.f);
+            for (int i2 = 0; i2 < 4; ++i2) {
+                uint32_t pw = rv[i2];
+                if constexpr (HASQ) {
+                    const uint32_t pq = ma_pack_bf16x2(ma_dq((wu >> (8 * i2)) & 15u, sc, ze),
+                                                       ma_dq((wu >> (8 * i2 + 4)) & 15u, sc, ze));
+                    pw = q ? pq : pw;
+                }
+                pw &= keep;
+                x[u][2 * i2] = __uint_as_float(pw << 16);
+                x[u][2 * i2 + 1] = __uint_as_float(pw & 0xffff0000u);
             }
         }
     }
