@@ -103,3 +103,30 @@ def test_fused_score_select_arguments_are_checked_on_the_host(lib):
         prefix_scores_topk(None, None, (None, None, None, None), [0], 1, value=False, rank="score")
     with pytest.raises(ValueError):
         prefix_scores_topk(None, None, (None, None, None, None), [0], 1, value=True, rank="keys")
+
+
+def test_packed_append_arguments_are_checked_on_the_host(lib):
+    """ma_append_packed rejects a split that is not whole key groups, a count that does not
+    add up, and mixed dtypes, before any launch."""
+    def t4(dtype=N.MA_BF16, ptr=16):
+        m = N.MaTensor4()
+        m.ptr, m.dtype = ptr, dtype
+        return m
+
+    z3, z4 = N.i64arr(0, 0, 0), N.i64arr(0, 0, 0, 0)
+    # move not a multiple of 32
+    rc = lib.ma_append_packed(t4(), t4(), 8, t4(), t4(), 1, 4, 32, 128, 16, 24, None, z4, None, None, z3, None, z4,
+                              None, None, z3, None)
+    assert rc == N.MA_EINVAL and b"move % 32" in lib.ma_last_error()
+    # move + keep != old_res + T
+    rc = lib.ma_append_packed(t4(), t4(), 8, t4(), t4(), 1, 4, 32, 128, 32, 16, None, z4, None, None, z3, None, z4,
+                              None, None, z3, None)
+    assert rc == N.MA_EINVAL
+    # residual in f32, new tokens in bf16
+    rc = lib.ma_append_packed(t4(N.MA_F32), t4(N.MA_F32), 8, t4(), t4(), 1, 4, 32, 128, 0, 40, None, z4, None, None,
+                              z3, None, z4, None, None, z3, None)
+    assert rc == N.MA_EINVAL and b"dtype" in lib.ma_last_error()
+    # quantizing with no planes
+    rc = lib.ma_append_packed(t4(), t4(), 0, t4(), t4(), 1, 4, 32, 128, 32, 0, None, z4, None, None, z3, None, z4,
+                              None, None, z3, None)
+    assert rc == N.MA_EINVAL and b"planes" in lib.ma_last_error()
