@@ -22,6 +22,7 @@ KernelUnavailableError.
 
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import torch
@@ -146,6 +147,11 @@ class PackedKVCache:
         gk = quant.key_token_group
         tokens = min(_ceil_to(self.max_tokens, gk), self._START_TOKENS)
         self._planes = self._plane_specs()
+        # bytes of one row (axis 3) of each plane over every layer and lane: the accounting
+        # below is arithmetic on the lengths, not tensor slicing
+        lanes = self.num_layers * self.batch_size * self.num_kv_heads
+        self._row_bytes = {name: lanes * math.prod(row) * torch.empty(0, dtype=dt).element_size()
+                           for name, (row, dt) in self._planes.items()}
         self._realloc(tokens=max(tokens, gk), residual=max(1, quant.residual_tokens + gk))
 
     # -- the plane table ----------------------------------------------------------------------
@@ -530,7 +536,6 @@ class PackedKVCache:
         on the device, to be raised by check_rebuild() -- called by the next rebuild -- instead
         of reading it back now."""
         from .kernels.rebuild import rebuild_packed
-        from .kernels.splitk import Prefix
 
         self.check_rebuild()
 
@@ -538,6 +543,8 @@ class PackedKVCache:
             raise RuntimeError("rebuild during an append")
         if self.k_q is None or self.v_q is None:
             raise ValueError("rebuild needs a packed (k_bits, v_bits < 16) cache")
+        if self.quant.k_bits != 4 or self.quant.v_bits != 4 or self.k_scale.dtype != torch.float16:
+            raise KernelUnavailableError("the packed rebuild is built for 4-bit codes with float16 scale / zero")
         lead = (self.num_layers, self.batch_size, self.num_kv_heads)
         lists = {"groups_before": groups_before, "encode": encode, "groups_after": groups_after, "stage": stage}
         for name, t in lists.items():
@@ -555,13 +562,9 @@ class PackedKVCache:
         self._realloc(tokens=_ceil_to(ql + st + 1024, gk), residual=max(st + 256, 64))
         remap = torch.empty(lead + (old_len,), device=self.device, dtype=torch.int64)
 
-        def prefix(p, nq, nf):
-            f = lambda n: p[n].flatten(0, 1)  # noqa: E731  (layers folded into the batch axis)
-            return Prefix(kq=f("k_q"), ks=f("k_scale"), kz=f("k_zero"), vq=f("v_q"), vs=f("v_scale"),
-                          vz=f("v_zero"), kf=f("k_residual"), vf=f("v_residual"), nq=nq, nf=nf, kb=4, vb=4)
-
         new_planes = {name: getattr(self, name) for name in self._planes}
-        status = rebuild_packed(prefix(old_planes, old_q, old_r), prefix(new_planes, ql, st), B=lead[0] * lead[1],
+        status = rebuild_packed(self._folded_native(old_planes, old_q, old_r), self._folded_native(new_planes, ql, st),
+                                B=lead[0] * lead[1],
                                 H=lead[2], D=self.head_dim, groups_before=groups_before, encode=encode,
                                 groups_after=groups_after, stage=stage, remap=remap, phys=phys, live=live,
                                 check=check)
@@ -570,6 +573,27 @@ class PackedKVCache:
         self.dropped += old_len - self.length
         self._note_peak()
         return remap
+
+    def _folded_native(self, planes: dict, nq: int, nf: int) -> N.MaPrefix:
+        """The C-ABI descriptor of whole 4-bit storage planes [L, B, H, ...] with the layers
+        folded into the batch axis (lane (l, b, h) = batch row l * B + b), as
+        ma_rebuild_packed reads the old storage and writes the new one.  The planes are this
+        cache's own allocations (contiguous; 4-bit codes and float16 scale / zero, as _rebuild
+        checks first), so the descriptor is filled from their strides without building views."""
+        kq, ks, kz, vq, vs, vz, kf, vf = (planes[x] for x in self._APPEND_PLANES)
+        p = N.MaPrefix()
+        p.nq, p.nf, p.kbits, p.vbits = int(nq), int(nf), 4, 4
+        p.kgroup, p.vgroup = self.quant.key_token_group, self.quant.value_channel_group
+        p.kq, p.ks, p.kz, p.vq, p.vs, p.vz = (t.data_ptr() for t in (kq, ks, kz, vq, vs, vz))
+        p.kf, p.vf = kf.data_ptr(), vf.data_ptr()
+        p.fdtype = N.dtype_code(kf.dtype)
+        p.skq[:] = kq.stride()[1:5]
+        p.svq[:] = vq.stride()[1:5]
+        p.sks[:] = ks.stride()[1:4]
+        p.svs[:] = vs.stride()[1:4]
+        p.skf[:] = kf.stride()[1:4]
+        p.svf[:] = vf.stride()[1:4]
+        return p
 
     # -- memory accounting --------------------------------------------------------------------
     def allocated_nbytes(self) -> int:
@@ -590,9 +614,8 @@ class PackedKVCache:
         out = dict.fromkeys(("key_payload", "key_metadata", "key_residual", "value_payload", "value_metadata",
                              "value_residual"), 0)
         for name in self._planes:
-            t = getattr(self, name)
-            rows = self._rows_in_use(_UNITS[name])
-            out[part[name]] += int(t[:, :, :, :rows].numel() * t.element_size())
+            rows = min(self._rows_in_use(_UNITS[name]), getattr(self, name).shape[3])
+            out[part[name]] += rows * self._row_bytes[name]
         out["total"] = sum(out.values())
         return out
 

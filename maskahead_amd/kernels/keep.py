@@ -12,6 +12,7 @@ reference runs on the keep path: ``EvictionState.survivors`` (eviction.py:325-40
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 
 import torch
@@ -174,6 +175,17 @@ def value_score_slots(a: torch.Tensor, prefix, slots: torch.Tensor, *, dtype: to
     return out
 
 
+def _rows_contiguous(shape, stride) -> bool:
+    """Whether the dims (shape, stride) after the token axis form one contiguous row (dims
+    of size 1 place no constraint)."""
+    want = 1
+    for size, st in zip(reversed(shape), reversed(stride)):
+        if size != 1 and st != want:
+            return False
+        want *= size
+    return True
+
+
 def compact_tokens(planes, keep: torch.Tensor, n: int) -> None:
     """In place, for every lane (b, h) and i < C: row i of every plane becomes its old
     row keep[b, h, i].  planes: tensors [B, H, n_cap, ...] (token axis 2; everything
@@ -195,17 +207,17 @@ def compact_tokens(planes, keep: torch.Tensor, n: int) -> None:
         group = planes[i:i + 8]
         bases, strides, rbytes = [], [], []
         for p in group:
-            if p.ndim < 3 or p.shape[0] != b or p.shape[1] != h or p.shape[2] < n:
-                raise ValueError(f"plane of shape {tuple(p.shape)} does not fit keep {tuple(keep.shape)} / n={n}")
+            shp, std = p.shape, p.stride()
+            if len(shp) < 3 or shp[0] != b or shp[1] != h or shp[2] < n:
+                raise ValueError(f"plane of shape {tuple(shp)} does not fit keep {tuple(keep.shape)} / n={n}")
             if p.device != keep.device:
                 raise ValueError("planes and keep must share a device")
-            inner = p[0, 0, 0]
-            if inner.numel() > 1 and not inner.is_contiguous():
+            if not _rows_contiguous(shp[3:], std[3:]):
                 raise ValueError("each token row of a plane must be contiguous")
             es = p.element_size()
             bases.append(p.data_ptr())
-            strides += [p.stride(0) * es, p.stride(1) * es, p.stride(2) * es]
-            rbytes.append(inner.numel() * es)
+            strides += [std[0] * es, std[1] * es, std[2] * es]
+            rbytes.append(math.prod(shp[3:]) * es)
         npl = len(group)
         base_arr = (ctypes.c_void_p * npl)(*bases)
         stride_arr = (ctypes.c_int64 * (3 * npl))(*strides)

@@ -88,22 +88,23 @@ def rebuild_plan_cut(launched, counts_host: torch.Tensor):
     """The lists of a rebuild_plan_launch, cut to the largest count of any lane; counts_host
     is its counts tensor read back to the host."""
     gb, enc, stg, _, lead = launched
-    c = counts_host.reshape(-1, 3)
-    if c.shape[0] == 0:
+    flat = counts_host.reshape(-1).tolist()           # a few hundred ints: host lists, no tensor ops
+    if not flat:
         empty = torch.empty((*lead, 0), device=gb.device, dtype=torch.int64)
         return empty, empty, empty
-    if bool((c < 0).any()):
+    if min(flat) < 0:
         raise N.KernelUnavailableError("rebuild plan: a lane holds more than 16384 live entries out of position "
                                        "order; only ordered lanes of that size are built")
-    g1, m, st = (int(x) for x in c.max(0).values)
+    g1, m, st = max(flat[0::3]), max(flat[1::3]), max(flat[2::3])
     return (gb[:, :g1].reshape(*lead, g1), enc[:, :m].reshape(*lead, m), stg[:, :st].reshape(*lead, st))
 
 
 def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Tensor, encode: torch.Tensor,
                    groups_after: torch.Tensor, stage: torch.Tensor, remap: torch.Tensor,
                    phys: torch.Tensor | None = None, live: int = 0, check: bool = True) -> torch.Tensor | None:
-    """One launch of ``ma_rebuild_packed``: old / new are Prefix descriptors of the storage
-    with layers folded into the batch axis (B = layers x batch); lists [lanes..., n]
+    """One launch of ``ma_rebuild_packed``: old / new are Prefix objects (or their built
+    MaPrefix descriptors) of the storage with layers folded into the batch axis (B =
+    layers x batch); lists [lanes..., n]
     int64; remap int64 [lanes..., old length] written whole; phys (optional) int32
     [lanes..., capacity] rewritten in place for its first ``live`` entries.  Raises
     RuntimeError for a list entry outside the old storage (as the reference's gathers
@@ -128,7 +129,8 @@ def rebuild_packed(old, new, *, B: int, H: int, D: int, groups_before: torch.Ten
         if phys.dtype != torch.int32 or p2.stride(-1) != 1 or p2.shape[1] < live:
             raise ValueError("phys must be int32 [lanes, capacity >= live] with contiguous rows")
         ph_ptr, ph_stride = p2.data_ptr(), p2.stride(0)
-    on, nn = old.native(), new.native()
+    on = old if isinstance(old, N.MaPrefix) else old.native()
+    nn = new if isinstance(new, N.MaPrefix) else new.native()
     gb, enc, ga, stg = lists
     N.call("ma_rebuild_packed", ctypes.byref(on), B, H, D, ctypes.byref(nn),
            gb.data_ptr(), _stride(gb), gb.shape[1], enc.data_ptr(), _stride(enc), enc.shape[1],

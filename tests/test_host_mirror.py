@@ -59,6 +59,19 @@ def test_cache_layouts_and_append_plan_cpu():
     assert b.residual_capacity == 0 and b.k_residual is None
     # accounting: nothing in use yet; every plane's bytes allocated
     assert c.logical_nbytes()["total"] == 0
+    # in use: the rows of each plane's unit (whole key groups, quantized tokens, residual),
+    # counted as the bytes of those rows' slices
+    c.length, c.quantized_length, c.residual_length = 1000, 960, 40
+    want = {}
+    for name, part in (("k_q", "key_payload"), ("k_scale", "key_metadata"), ("k_zero", "key_metadata"),
+                       ("k_residual", "key_residual"), ("v_q", "value_payload"), ("v_scale", "value_metadata"),
+                       ("v_zero", "value_metadata"), ("v_residual", "value_residual")):
+        t = getattr(c, name)
+        rows = {"k_q": 30, "k_scale": 30, "k_zero": 30, "k_residual": 40}.get(name, 960 if "residual" not in name else 40)
+        want[part] = want.get(part, 0) + t[:, :, :, :rows].numel() * t.element_size()
+    got = c.logical_nbytes()
+    assert all(got[x] == want[x] for x in want) and got["total"] == sum(want.values())
+    c.length = c.quantized_length = c.residual_length = 0
     assert c.allocated_nbytes() == sum(t.numel() * t.element_size() for t in (c.k_q, c.k_scale, c.k_zero, c.v_q,
                                                                                c.v_scale, c.v_zero, c.k_residual,
                                                                                c.v_residual))
@@ -190,3 +203,18 @@ def test_admitting_entries_after_a_compaction():
     wrong.append(range(1000, 1032))                               # positions as slots
     with pytest.raises(ValueError, match="outside the cache"):
         live_slot_masks(cache, wrong)
+
+
+def test_rows_contiguous():
+    """The per-plane row check of compact_tokens: the dims after the token axis must form
+    one contiguous row; dims of size 1 place no constraint."""
+    from maskahead_amd.kernels.keep import _rows_contiguous
+
+    t = torch.zeros(2, 3, 10, 4, 5)
+    assert _rows_contiguous(t.shape[3:], t.stride()[3:])
+    assert _rows_contiguous((), ())
+    tt = t.transpose(3, 4)
+    assert not _rows_contiguous(tt.shape[3:], tt.stride()[3:])
+    assert _rows_contiguous((1, 5), (999, 1))
+    s = t[..., ::2]
+    assert not _rows_contiguous(s.shape[3:], s.stride()[3:])
