@@ -142,6 +142,7 @@ class PackedKVCache:
         self.planes_generation = 0
         self._pending_rebuild_status: torch.Tensor | None = None   # a rebuild's unread errors
         self._append_geo: tuple | None = None     # ma_append_packed's plane geometry (_append_packed)
+        self._append_kv: tuple | None = None      # and its new tokens' descriptors
         for name in _UNITS:
             setattr(self, name, None)
         gk = quant.key_token_group
@@ -276,8 +277,6 @@ class PackedKVCache:
         """Write one layer's new entries: 16-bit planes get them at [length, length + T) by
         the append kernel; packed planes quantize the whole key groups of [residual | new]
         and keep the rest as the residual."""
-        from .kernels.ops import quantize_key_groups_into, quantize_values_into
-
         plan = self._append_plan
         if plan is None:
             raise RuntimeError("begin_append must be called before stage_layer")
@@ -295,6 +294,8 @@ class PackedKVCache:
         if self.quant.packed and self._append_fused(key, value):
             self._append_packed(layer_idx, plan, key, value)
         elif self.quant.packed:
+            from .kernels.ops import quantize_key_groups_into, quantize_values_into
+
             move, keep = plan.quantize_from_residual, plan.new_residual
             k_tail = self._tail(self.k_residual[layer_idx], plan.old_residual, key)
             v_tail = self._tail(self.v_residual[layer_idx], plan.old_residual, value)
@@ -352,10 +353,18 @@ class PackedKVCache:
             return base + layer_idx * per_layer + row * per_row
 
         kres.ptr, vres.ptr = at(6, 0), at(7, 0)
-        b, h, t, d = key.shape
-        N.call("ma_append_packed", kres, vres, plan.old_residual, N.t4(key), N.t4(value), b, h, t, d, move, keep,
-               at(0, g0), arrs[0], at(1, g0), at(2, g0), arrs[1], at(3, t0), arrs[2], at(4, t0), at(5, t0), arrs[3],
-               N.stream_of(key))
+        # the new tokens' descriptors are kept while their geometry is the same (a decode
+        # loop stages same-shaped blocks): only the two addresses change
+        kv = (key.shape, key.stride(), key.dtype, value.stride(), value.dtype)
+        hit = self._append_kv
+        if hit is None or hit[0] != kv:
+            hit = self._append_kv = (kv, N.t4(key), N.t4(value), N.load().ma_append_packed)
+        _, kt, vt, fn = hit
+        kt.ptr, vt.ptr = key.data_ptr(), value.data_ptr()
+        b, h, t, d = kv[0]
+        N.check(fn(kres, vres, plan.old_residual, kt, vt, b, h, t, d, move, keep, at(0, g0), arrs[0], at(1, g0),
+                   at(2, g0), arrs[1], at(3, t0), arrs[2], at(4, t0), at(5, t0), arrs[3], N.stream_of(key)),
+                "ma_append_packed")
 
     def _tail(self, residual: torch.Tensor, old: int, new: torch.Tensor) -> torch.Tensor:
         """[residual rows 0..old | new] as one compute-dtype tensor (a copy when old > 0)."""
