@@ -225,6 +225,11 @@ struct StoreDev {
     int64_t skq[4], sks[3], svq[4], svs[3], skr[3], svr[3];
 };
 
+// DC 0: any layout, the strides inside a lane read from the descriptor.  DC 64 or 128: a
+// store of that head_dim laid out as the cache allocates it (a key group's rows 16 B
+// apart, its scales contiguous, value groups of 16 B, scales and residual rows dense),
+// so every stride inside a lane is a compile-time constant (ma_rebuild_packed checks).
+template <int DC>
 __device__ __forceinline__ LaneStore lane_store(const StoreDev &s, int b, int h) {
     LaneStore L;
     L.kq = s.kq ? s.kq + b * s.skq[0] + h * s.skq[1] : nullptr;
@@ -235,14 +240,25 @@ __device__ __forceinline__ LaneStore lane_store(const StoreDev &s, int b, int h)
     L.vz = s.vz ? s.vz + b * s.svs[0] + h * s.svs[1] : nullptr;
     L.kr = s.kr ? s.kr + b * s.skr[0] + h * s.skr[1] : nullptr;
     L.vr = s.vr ? s.vr + b * s.svr[0] + h * s.svr[1] : nullptr;
-    L.kq_g = s.skq[2];
-    L.kq_d = s.skq[3];
-    L.ks_g = s.sks[2];
-    L.vq_n = s.svq[2];
-    L.vq_c = s.svq[3];
-    L.vs_n = s.svs[2];
-    L.kr_n = s.skr[2];
-    L.vr_n = s.svr[2];
+    if constexpr (DC > 0) {
+        L.kq_g = DC * 16;
+        L.kq_d = 16;
+        L.ks_g = DC;
+        L.vq_n = DC / 2;
+        L.vq_c = 16;
+        L.vs_n = DC / VG;
+        L.kr_n = DC;
+        L.vr_n = DC;
+    } else {
+        L.kq_g = s.skq[2];
+        L.kq_d = s.skq[3];
+        L.ks_g = s.sks[2];
+        L.vq_n = s.svq[2];
+        L.vq_c = s.svq[3];
+        L.vs_n = s.svs[2];
+        L.kr_n = s.skr[2];
+        L.vr_n = s.svr[2];
+    }
     return L;
 }
 
@@ -262,33 +278,52 @@ struct RbArgs {
 
 // Old entry `src` of a lane as bf16-rounded floats, channels d0 .. d0+7: the dequantized
 // packed entry (reference.py:168-179, 259-268, then the bf16 cast of dequantize_layer)
-// or the bf16 residual; an invalid slot (-1 padding, or out of range) is zeros.
-__device__ __forceinline__ void old_entry8(const RbArgs &a, const LaneStore &o, int64_t src, int d0, float *k8,
+// or the bf16 residual; an invalid slot (-1 padding, or out of range) is zeros.  DC > 0:
+// the 8 key scales (and zeros) are one 16-byte load, the 8 code bytes constant offsets.
+template <int DC>
+__device__ __forceinline__ void old_entry8(const RbArgs &a, const LaneStore &o, int64_t src64, int d0, float *k8,
                                            float *v8) {
-    if (src < 0 || src >= a.old_len) {
+    if (src64 < 0 || src64 >= a.old_len) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) k8[i] = v8[i] = 0.f;
         return;
     }
+    const int src = (int)src64;   // < old_len, an int
     if (src < a.old_ql) {
-        const int64_t g = src / KG;
-        const int t = (int)(src % KG);
-        const uint8_t *kb = o.kq + g * o.kq_g + (t >> 1);
+        const int g = src / KG, t = src % KG;
+        const uint8_t *kb = o.kq + (int64_t)g * o.kq_g + (int64_t)d0 * o.kq_d + (t >> 1);
+        const int64_t so = (int64_t)g * o.ks_g + d0;
+        uint16_t sc[8], ze[8];
+        if constexpr (DC > 0) {
+            const uint4 sw = *(const uint4 *)(o.ks + so), zw = *(const uint4 *)(o.kz + so);
+            const uint32_t s4[4] = {sw.x, sw.y, sw.z, sw.w}, z4[4] = {zw.x, zw.y, zw.z, zw.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[2 * i] = (uint16_t)(s4[i] & 0xffffu);
+                sc[2 * i + 1] = (uint16_t)(s4[i] >> 16);
+                ze[2 * i] = (uint16_t)(z4[i] & 0xffffu);
+                ze[2 * i + 1] = (uint16_t)(z4[i] >> 16);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sc[i] = o.ks[so + i];
+                ze[i] = o.kz[so + i];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int d = d0 + i;
-            const uint32_t byte = kb[(int64_t)d * o.kq_d];
+            const uint32_t byte = kb[(int64_t)i * o.kq_d];
             const uint32_t code = (t & 1) ? (byte >> 4) : (byte & 15u);
-            const int64_t so = g * o.ks_g + d;
-            k8[i] = ma_round_bf16(ma_dq(code, ma_f16_to_f32(o.ks[so]), ma_f16_to_f32(o.kz[so])));
+            k8[i] = ma_round_bf16(ma_dq(code, ma_f16_to_f32(sc[i]), ma_f16_to_f32(ze[i])));
         }
         const int c = d0 / VG;
-        const uint8_t *vb = o.vq + src * o.vq_n + c * o.vq_c + (d0 % VG) / 2;
+        const uint8_t *vb = o.vq + (int64_t)src * o.vq_n + c * o.vq_c + (d0 % VG) / 2;
         const uint32_t w = *(const uint32_t *)vb;   // 4 bytes = channels d0 .. d0+7
-        const int64_t so = src * o.vs_n + c;
-        const float sc = ma_f16_to_f32(o.vs[so]), ze = ma_f16_to_f32(o.vz[so]);
+        const int64_t vso = (int64_t)src * o.vs_n + c;
+        const float vsc = ma_f16_to_f32(o.vs[vso]), vze = ma_f16_to_f32(o.vz[vso]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v8[i] = ma_round_bf16(ma_dq((w >> (4 * i)) & 15u, sc, ze));
+        for (int i = 0; i < 8; ++i) v8[i] = ma_round_bf16(ma_dq((w >> (4 * i)) & 15u, vsc, vze));
         return;
     }
     const int64_t r = src - a.old_ql;
@@ -390,8 +425,9 @@ __global__ void __launch_bounds__(RM_THREADS) remap_kernel(RbArgs a) {
 
 // New group `dst` of a lane: old group `src` copied byte for byte (kept / tail groups;
 // padding copies group 0, as the reference gathers clamped ids).
+template <int DC>
 __device__ void copy_group(const RbArgs &a, const LaneStore &o, const LaneStore &n, int64_t src, int dst) {
-    const int tid = threadIdx.x, D = a.D, ncg = D / VG;
+    const int tid = threadIdx.x, D = DC > 0 ? DC : a.D, ncg = D / VG;
     if (src < 0 || src >= a.old_ng) src = 0;
     for (int d = tid; d < D; d += RB_THREADS) {
         *(uint4 *)(n.kq + dst * n.kq_g + d * n.kq_d) = *(const uint4 *)(o.kq + src * o.kq_g + d * o.kq_d);
@@ -415,15 +451,16 @@ __device__ void copy_group(const RbArgs &a, const LaneStore &o, const LaneStore 
 // exchanges and each lane quantizes its 8 channels in registers.  Keys go through LDS
 // (one column per channel) and are quantized by P = 256 / D adjacent lanes per channel,
 // 32 / P tokens each, their ranges combined the same way.
+template <int DC>
 __device__ void encode_group(const RbArgs &a, const LaneStore &o, const LaneStore &n, int lane, int j) {
     __shared__ float xk[KG][129];   // head_dim <= 128 (+1: column reads across rows)
-    const int tid = threadIdx.x, D = a.D, oct = D / 8;
+    const int tid = threadIdx.x, D = DC > 0 ? DC : a.D, oct = D / 8;
     const int g = a.g1 + j;
     for (int u = tid; u < KG * oct; u += RB_THREADS) {
         const int t = u / oct, oc = u % oct, d0 = oc * 8;
         const int64_t src = list_at(a.enc, a.senc, lane, a.m, j * KG + t);
         float k8[8], v8[8];
-        old_entry8(a, o, src, d0, k8, v8);
+        old_entry8<DC>(a, o, src, d0, k8, v8);
 #pragma unroll
         for (int i = 0; i < 8; ++i) xk[t][d0 + i] = k8[i];
         // the value group of channels 32 c .. 32 c + 31: lanes with octets 4c .. 4c + 3 (oct
@@ -479,14 +516,15 @@ __device__ void encode_group(const RbArgs &a, const LaneStore &o, const LaneStor
 
 // Staged entries 32 c .. 32 c + 31 of a lane: old entries as bf16 rows of the new
 // residual (zeros for padding).
+template <int DC>
 __device__ void stage_chunk(const RbArgs &a, const LaneStore &o, const LaneStore &n, int lane, int c) {
-    const int tid = threadIdx.x, oct = a.D / 8;
+    const int tid = threadIdx.x, oct = (DC > 0 ? DC : a.D) / 8;
     for (int u = tid; u < KG * oct; u += RB_THREADS) {
         const int t = c * KG + u / oct, d0 = (u % oct) * 8;
         if (t >= a.st) continue;
         const int64_t src = list_at(a.stg, a.sstg, lane, a.st, t);
         float k8[8], v8[8];
-        old_entry8(a, o, src, d0, k8, v8);
+        old_entry8<DC>(a, o, src, d0, k8, v8);
         uint4 kw, vw;
         kw.x = ma_pack_bf16x2(k8[0], k8[1]);
         kw.y = ma_pack_bf16x2(k8[2], k8[3]);
@@ -505,42 +543,44 @@ __device__ void stage_chunk(const RbArgs &a, const LaneStore &o, const LaneStore
 // [stage: lanes x ceil(st/32)]; the remap itself follows in remap_kernel.
 constexpr int FILL_PER_BLOCK = RB_THREADS * 16;
 
+template <int DC>
 __global__ void __launch_bounds__(RB_THREADS) rebuild_kernel(RbArgs a) {
-    int64_t idx = blockIdx.x;
-    const int nfill = (a.old_len + FILL_PER_BLOCK - 1) / FILL_PER_BLOCK;
-    if (idx < (int64_t)a.lanes * nfill) {
+    // 32-bit workgroup arithmetic: the host keeps the grid below 2^31 workgroups
+    uint32_t idx = blockIdx.x;
+    const uint32_t nfill = (uint32_t)((a.old_len + FILL_PER_BLOCK - 1) / FILL_PER_BLOCK);
+    if (idx < (uint32_t)a.lanes * nfill) {
         const int lane = (int)(idx / nfill), c = (int)(idx % nfill);
         int64_t *rm = a.remap + lane * a.sremap;
         const int end = min(a.old_len, (c + 1) * FILL_PER_BLOCK);
         for (int i = c * FILL_PER_BLOCK + threadIdx.x; i < end; i += RB_THREADS) rm[i] = -1;
         return;
     }
-    idx -= (int64_t)a.lanes * nfill;
-    const int ncopy = a.g1 + a.g3, nstc = (a.st + KG - 1) / KG;
+    idx -= (uint32_t)a.lanes * nfill;
+    const uint32_t ncopy = (uint32_t)(a.g1 + a.g3), g2 = (uint32_t)a.g2, nstc = (uint32_t)((a.st + KG - 1) / KG);
     int lane, kind, j;
-    if (idx < (int64_t)a.lanes * ncopy) {
+    if (idx < (uint32_t)a.lanes * ncopy) {
         kind = 0;
         lane = (int)(idx / ncopy);
         j = (int)(idx % ncopy);
-    } else if ((idx -= (int64_t)a.lanes * ncopy) < (int64_t)a.lanes * a.g2) {
+    } else if ((idx -= (uint32_t)a.lanes * ncopy) < (uint32_t)a.lanes * g2) {
         kind = 1;
-        lane = (int)(idx / a.g2);
-        j = (int)(idx % a.g2);
+        lane = (int)(idx / g2);
+        j = (int)(idx % g2);
     } else {
-        idx -= (int64_t)a.lanes * a.g2;
+        idx -= (uint32_t)a.lanes * g2;
         kind = 2;
         lane = (int)(idx / nstc);
         j = (int)(idx % nstc);
     }
     const int b = lane / a.H, h = lane % a.H;
-    const LaneStore o = lane_store(a.old, b, h), n = lane_store(a.nw, b, h);
+    const LaneStore o = lane_store<DC>(a.old, b, h), n = lane_store<DC>(a.nw, b, h);
     if (kind == 0) {
         const int64_t src = j < a.g1 ? list_at(a.gb, a.sgb, lane, a.g1, j) : list_at(a.ga, a.sga, lane, a.g3, j - a.g1);
-        copy_group(a, o, n, src, j < a.g1 ? j : a.g1 + a.g2 + (j - a.g1));
+        copy_group<DC>(a, o, n, src, j < a.g1 ? j : a.g1 + a.g2 + (j - a.g1));
     } else if (kind == 1) {
-        encode_group(a, o, n, lane, j);
+        encode_group<DC>(a, o, n, lane, j);
     } else {
-        stage_chunk(a, o, n, lane, j);
+        stage_chunk<DC>(a, o, n, lane, j);
     }
 }
 
@@ -724,8 +764,17 @@ extern "C" int ma_rebuild_packed(const ma_prefix *old_store, int B, int H, int D
         ma_set_error("%s: grid of %lld workgroups too large", who, (long long)blocks);
         return MA_EINVAL;
     }
-    if (blocks > 0)
-        hipLaunchKernelGGL(rebuild_kernel, dim3((unsigned)blocks), dim3(RB_THREADS), 0, (hipStream_t)stream, a);
+    // the cache's own layout (both stores): the instantiation with constant inner strides
+    auto dense = [D](const ma_prefix *p) {
+        const bool al16 = !(((uintptr_t)p->ks | (uintptr_t)p->kz) & 15) && !((p->sks[0] | p->sks[1]) & 7);
+        return al16 && p->skq[3] == 16 && p->skq[2] == (int64_t)D * 16 && p->sks[2] == D && p->svq[3] == 16 &&
+               p->svq[2] == D / 2 && p->svs[2] == D / VG && p->skf[2] == D && p->svf[2] == D;
+    };
+    const int dc = (D == 64 || D == 128) && dense(old_store) && dense(new_store) ? D : 0;
+    if (blocks > 0) {
+        auto kern = dc == 128 ? rebuild_kernel<128> : dc == 64 ? rebuild_kernel<64> : rebuild_kernel<0>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(RB_THREADS), 0, (hipStream_t)stream, a);
+    }
     rc = ma_check_launch(who);
     if (rc) return rc;
     hipLaunchKernelGGL(remap_kernel, dim3(lanes), dim3(RM_THREADS), 0, (hipStream_t)stream, a);
