@@ -187,6 +187,68 @@ def test_rebuild_direct_lists_and_errors(gpu):
     _check_cache(cache, want, want_lens)
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_rebuild_any_layout_equals_cache_layout(gpu, D):
+    """ma_rebuild_packed has an instantiation for stores laid out as the cache allocates
+    them (constant strides inside a lane) and one reading every stride from the
+    descriptor.  Old storage with padded inner dimensions (so the general one runs) and
+    the cache's own layout give the oracle's bytes, bit for bit."""
+    from maskahead_amd.kernels.rebuild import rebuild_packed
+    from maskahead_amd.kernels.splitk import Prefix
+
+    L, H, n_q, n_r = 2, 2, 1024, 32
+    store, lens, g = _random_cache(31 + D, L=L, H=H, D=D, n_q=n_q, n_r=n_r)
+    n = lens[0]
+    gb = torch.tensor([[3, 7, 30], [0, 12, -1], [5, 6, 8], [31, 1, 2]]).view(L, 1, H, 3)
+    enc = torch.stack([torch.randperm(n, generator=g)[:75].sort().values for _ in range(L * H)]).view(L, 1, H, 75)
+    enc[1, 0, 1, 70:] = -1
+    ga = torch.empty((L, 1, H, 0), dtype=torch.int64)
+    stg = torch.stack([torch.randperm(n, generator=g)[:20].sort().values for _ in range(L * H)]).view(L, 1, H, 20)
+    want, want_lens, want_remap = OR.rebuild(store, lens, gb, enc, ga, stg)
+    nql, st = want_lens[1], want_lens[2]
+
+    def planes(src, pad):
+        """src (oracle layout) on the GPU; pad: dimension 4 widened (by 2 rows of codes or
+        scales, by 8 residual channels, so rows stay as aligned as the library requires)
+        and the original extent viewed: the same values, strides the cache never makes."""
+        out = {}
+        for short, _ in NAMES:
+            t = src[short]
+            if pad:
+                w = 8 if short in ("kr", "vr") else 2
+                big = torch.zeros([x + (w if i == 4 else 0) for i, x in enumerate(t.shape)], dtype=t.dtype)
+                big[tuple(slice(0, x) for x in t.shape)] = t
+                t = big.to(gpu)[tuple(slice(0, x) for x in t.shape)]
+            else:
+                t = t.to(gpu)
+            out[short] = t
+        return out
+
+    def prefix(p, nq, nf):
+        f = lambda x: p[x].flatten(0, 1)  # noqa: E731
+        return Prefix(kq=f("kq"), ks=f("ks"), kz=f("kz"), vq=f("vq"), vs=f("vs"), vz=f("vz"), kf=f("kr"), vf=f("vr"),
+                      nq=nq, nf=nf, kb=4, vb=4)
+
+    empty = {"kq": torch.zeros((L, 1, H, nql // 32, D, 16), dtype=torch.uint8),
+             "ks": torch.zeros((L, 1, H, nql // 32, D), dtype=torch.float16),
+             "kz": torch.zeros((L, 1, H, nql // 32, D), dtype=torch.float16),
+             "vq": torch.zeros((L, 1, H, nql, D // 32, 16), dtype=torch.uint8),
+             "vs": torch.zeros((L, 1, H, nql, D // 32), dtype=torch.float16),
+             "vz": torch.zeros((L, 1, H, nql, D // 32), dtype=torch.float16),
+             "kr": torch.zeros((L, 1, H, st, D), dtype=torch.bfloat16),
+             "vr": torch.zeros((L, 1, H, st, D), dtype=torch.bfloat16)}
+    for pad in (True, False):
+        old, new = planes(store, pad), planes(empty, False)
+        remap = torch.empty((L, 1, H, n), dtype=torch.int64, device=gpu)
+        assert (old["ks"].stride(4) == 1) and (old["ks"].stride(3) == (D + 2 if pad else D))
+        rebuild_packed(prefix(old, n_q, n_r), prefix(new, nql, st), B=L, H=H, D=D, groups_before=gb.to(gpu),
+                       encode=enc.to(gpu), groups_after=ga.to(gpu), stage=stg.to(gpu), remap=remap)
+        torch.cuda.synchronize()
+        for short, _ in NAMES:
+            assert same_bits(new[short].cpu(), want[short]), (pad, short)
+        assert torch.equal(remap.cpu(), want_remap), pad
+
+
 def test_evict_to_bf16_cache_with_tail(gpu):
     """A 16-bit cache (session.py:292-296): the live slots, then a stored-but-unadmitted
     tail, gathered exactly in place; the state's slots become 0 .. live - 1."""
