@@ -218,3 +218,24 @@ def test_rows_contiguous():
     assert _rows_contiguous((1, 5), (999, 1))
     s = t[..., ::2]
     assert not _rows_contiguous(s.shape[3:], s.stride()[3:])
+
+
+def test_rebuild_plan_cut_host():
+    """The plan's lists are cut to the largest count of any lane (groups, encoded, staged)
+    from the counts read back to the host; a negative count (a lane the plan could not
+    order) raises KernelUnavailableError."""
+    from maskahead_amd.kernels.rebuild import rebuild_plan_cut
+
+    lead = (2, 1, 2)
+    gb = torch.arange(4 * 10).view(4, 10)
+    enc = torch.arange(4 * 50).view(4, 50)
+    stg = torch.arange(4 * 50).view(4, 50) + 1000
+    counts = torch.tensor([[3, 40, 0], [7, 12, 5], [1, 0, 2], [0, 33, 1]], dtype=torch.int32)
+    g, e, s = rebuild_plan_cut((gb, enc, stg, None, lead), counts)
+    assert g.shape == (2, 1, 2, 7) and e.shape == (2, 1, 2, 40) and s.shape == (2, 1, 2, 5)
+    assert torch.equal(g.reshape(4, 7), gb[:, :7]) and torch.equal(s.reshape(4, 5), stg[:, :5])
+    counts[2, 1] = -1
+    with pytest.raises(KernelUnavailableError):
+        rebuild_plan_cut((gb, enc, stg, None, lead), counts)
+    empty = rebuild_plan_cut((gb[:0], enc[:0], stg[:0], None, (0, 1, 2)), counts[:0])
+    assert all(t.shape == (0, 1, 2, 0) for t in empty)
