@@ -15,12 +15,11 @@
 //                   live entry classified in (position, slot) order -- the order the lanes
 //                   already hold after a keep-set selection, so the sort is skipped; lanes
 //                   out of that order are sorted in LDS (bitonic, up to 16384 entries).
-// ma_rebuild_packed two launches.  The first: 256-thread workgroups that fill the slot
-//                   remap with -1, copy a kept group byte for byte, requantize a new group
-//                   or gather 32 staged bf16 entries.  The second: one 1024-thread
-//                   workgroup per lane scatters the new slots into the remap in the
-//                   reference's list order and rewrites the eviction state's slots
-//                   through it.  Old and new storage never alias.
+// ma_rebuild_packed one launch of 256-thread workgroups: one per lane fills the slot remap
+//                   with -1, scatters the new slots into it in the reference's list order
+//                   and rewrites the eviction state's slots through it; the others copy a
+//                   kept group byte for byte, requantize a new group or gather 32 staged
+//                   bf16 entries.  Old and new storage never alias.
 #include "ma_common.h"
 #include "ma_quant.h"
 
@@ -344,20 +343,24 @@ __device__ __forceinline__ int64_t list_at(const int64_t *p, int64_t stride, int
     return i < n ? p[lane * stride + i] : -1;
 }
 
-// Per lane, after the fill of the data launch: remap[old slot] = new slot, written in the
-// reference's order (kept and tail groups, encoded, staged: a later list wins a slot
-// named twice), then the eviction state's slots rewritten through it.  Each thread loads
+// One workgroup per lane, inside the data launch (it reads only the lists and the
+// state's slots, never the storage): every old slot's remap set to -1, then remap[old
+// slot] = new slot written in the reference's order (kept and tail groups, encoded,
+// staged: a later list wins a slot named twice, the workgroup's barriers ordering its
+// stores), then the eviction state's slots rewritten through it.  Each thread loads
 // RM_BATCH list entries before it stores any, so a phase costs about one round trip.
 // status bit 0: a list names a slot or group outside the old storage; bit 1: a live
 // entry's slot maps to no new slot.
-constexpr int RM_THREADS = 1024;
+constexpr int RM_THREADS = RB_THREADS;
 constexpr int RM_BATCH = 8;
 
-__global__ void __launch_bounds__(RM_THREADS) remap_kernel(RbArgs a) {
+__device__ void remap_lane(const RbArgs &a, int lane) {
     __shared__ int flags;
-    const int lane = blockIdx.x, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     int64_t *rm = a.remap + lane * a.sremap;
     if (tid == 0) flags = 0;
+    for (int i = tid; i < a.old_len; i += RM_THREADS) rm[i] = -1;
+    __syncthreads();
     int bad = 0;
     // kept and tail groups: every slot of a copied group, dead ones included
     const int ngi = (a.g1 + a.g3) * KG;
@@ -539,23 +542,18 @@ __device__ void stage_chunk(const RbArgs &a, const LaneStore &o, const LaneStore
     }
 }
 
-// grid: [remap fill: lanes x nfill] [copy: lanes x (g1 + g3)] [encode: lanes x g2]
-// [stage: lanes x ceil(st/32)]; the remap itself follows in remap_kernel.
-constexpr int FILL_PER_BLOCK = RB_THREADS * 16;
+// grid: [remap: lanes] [copy: lanes x (g1 + g3)] [encode: lanes x g2] [stage: lanes x
+// ceil(st/32)]: the remap workgroups first, so they run beside the requantization.
 
 template <int DC>
 __global__ void __launch_bounds__(RB_THREADS) rebuild_kernel(RbArgs a) {
     // 32-bit workgroup arithmetic: the host keeps the grid below 2^31 workgroups
     uint32_t idx = blockIdx.x;
-    const uint32_t nfill = (uint32_t)((a.old_len + FILL_PER_BLOCK - 1) / FILL_PER_BLOCK);
-    if (idx < (uint32_t)a.lanes * nfill) {
-        const int lane = (int)(idx / nfill), c = (int)(idx % nfill);
-        int64_t *rm = a.remap + lane * a.sremap;
-        const int end = min(a.old_len, (c + 1) * FILL_PER_BLOCK);
-        for (int i = c * FILL_PER_BLOCK + threadIdx.x; i < end; i += RB_THREADS) rm[i] = -1;
+    if (idx < (uint32_t)a.lanes) {
+        remap_lane(a, (int)idx);
         return;
     }
-    idx -= (uint32_t)a.lanes * nfill;
+    idx -= (uint32_t)a.lanes;
     const uint32_t ncopy = (uint32_t)(a.g1 + a.g3), g2 = (uint32_t)a.g2, nstc = (uint32_t)((a.st + KG - 1) / KG);
     int lane, kind, j;
     if (idx < (uint32_t)a.lanes * ncopy) {
@@ -758,8 +756,7 @@ extern "C" int ma_rebuild_packed(const ma_prefix *old_store, int B, int H, int D
         ma_set_error("%s: key groups to copy but the old storage has none", who);
         return MA_EINVAL;
     }
-    const int64_t nfill = (old_len + FILL_PER_BLOCK - 1) / FILL_PER_BLOCK;
-    const int64_t blocks = (int64_t)lanes * (nfill + g1 + g3 + g2 + (st + KG - 1) / KG);
+    const int64_t blocks = (int64_t)lanes * (1 + g1 + g3 + g2 + (st + KG - 1) / KG);
     if (blocks > 0x7fffffff) {
         ma_set_error("%s: grid of %lld workgroups too large", who, (long long)blocks);
         return MA_EINVAL;
@@ -771,12 +768,7 @@ extern "C" int ma_rebuild_packed(const ma_prefix *old_store, int B, int H, int D
                p->svq[2] == D / 2 && p->svs[2] == D / VG && p->skf[2] == D && p->svf[2] == D;
     };
     const int dc = (D == 64 || D == 128) && dense(old_store) && dense(new_store) ? D : 0;
-    if (blocks > 0) {
-        auto kern = dc == 128 ? rebuild_kernel<128> : dc == 64 ? rebuild_kernel<64> : rebuild_kernel<0>;
-        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(RB_THREADS), 0, (hipStream_t)stream, a);
-    }
-    rc = ma_check_launch(who);
-    if (rc) return rc;
-    hipLaunchKernelGGL(remap_kernel, dim3(lanes), dim3(RM_THREADS), 0, (hipStream_t)stream, a);
+    auto kern = dc == 128 ? rebuild_kernel<128> : dc == 64 ? rebuild_kernel<64> : rebuild_kernel<0>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(RB_THREADS), 0, (hipStream_t)stream, a);
     return ma_check_launch(who);
 }
