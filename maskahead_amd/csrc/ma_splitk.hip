@@ -621,20 +621,12 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
             }
-#ifndef X_NOPV
             pv_regs<D>(S.u.t.vt[cb].vt, pb, acc, c32, hf);
-#else
-            acc[0][0] += (float)pb[0][0] + (float)pb[1][1] + (float)pb[2][2] + (float)pb[3][3];
-#endif
         }
-#ifndef X_NOSTAGE
         if (it + 2 < nt) {
             store_tile((it + 2) % NBUF);
-#ifndef X_NOLOAD
             if (it + 3 < nt) load_tile(it + 3);
-#endif
         }
-#endif
         __syncthreads();
     };
     int it = 0;
