@@ -456,6 +456,21 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
         else if (!is_k && vl < Shape::NV) item_off = v_item_offsets<D>(L, vl);
     }
     const bool fast_tiles = SRC == 0 && (FULL || !L.mask);
+    // all-bf16 dense source without a slot mask: the byte offset of this thread's first
+    // item from a whole tile's first token, computed once (a whole tile then costs one base
+    // address per operand and no bounds checks).  Item r of a K lane is KLANES / (D / 8) * r
+    // tokens further, item r of a V lane 8 r channels further (its second token one row
+    // on): wave-uniform steps.  32-bit while 64 rows span < 2 GiB.
+    uint32_t doff = 0u;
+    bool dense_fast = false;
+    if constexpr (SRC == 2) {
+        static_assert(KLANES % (D / 8) == 0 && KLANES % (TILE / 2) == 0, "item steps are whole rows / chunks");
+        const int64_t sn = is_k ? ds.sk : ds.sv;
+        dense_fast = !ds.mask && sn >= 0 && sn * 2 * TILE < (int64_t)0x7fffffff;
+        const int t = is_k ? kl / (D / 8) : 2 * (vl % (TILE / 2));
+        const int chk = is_k ? kl % (D / 8) : vl / (TILE / 2);
+        doff = (uint32_t)(((int64_t)t * sn + chk * 8) * 2);
+    }
     auto load_k = [&](int i) {
         const int n0 = tile_n0(i);
         if constexpr (SRC == 0) {
@@ -476,6 +491,23 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         } else {
             const char *base = ds.k + (int64_t)(n0 - ds.tok0) * ds.sk * ds.esz;
+            if constexpr (SRC == 2) {
+                if (dense_fast && n0 + TILE <= n_end) {
+                    const int64_t kstep = (int64_t)(KLANES / (D / 8)) * ds.sk * 2;
+#pragma unroll
+                    for (int r = 0; r < Shape::KPL; ++r) {
+                        if (kl + r * KLANES < Shape::NK) {
+                            const uint4 q = *(const uint4 *)(base + r * kstep + doff);
+                            pr.w[4 * r] = q.x;
+                            pr.w[4 * r + 1] = q.y;
+                            pr.w[4 * r + 2] = q.z;
+                            pr.w[4 * r + 3] = q.w;
+                        }
+                    }
+                    pr.flags |= (1u << Shape::KPL) - 1u;
+                    return;
+                }
+            }
 #pragma unroll
             for (int r = 0; r < Shape::KPL; ++r) {
                 const int u = kl + r * KLANES;
@@ -515,6 +547,28 @@ __global__ void __launch_bounds__(NTH) splitk_fwd_kernel(FwdArgs a) {
             }
         } else {
             const char *base = ds.v + (int64_t)(n0 - ds.tok0) * ds.sv * ds.esz;
+            if constexpr (SRC == 2) {
+                if (dense_fast && n0 + TILE <= n_end) {
+#pragma unroll
+                    for (int r = 0; r < Shape::VPL; ++r) {
+                        if (vl + r * KLANES < Shape::NV) {
+                            const char *pa = base + r * (KLANES / (TILE / 2)) * 16 + doff;
+                            const uint4 qa = *(const uint4 *)pa;
+                            const uint4 qb = *(const uint4 *)(pa + ds.sv * 2);
+                            pr.w[8 * r] = qa.x;
+                            pr.w[8 * r + 1] = qa.y;
+                            pr.w[8 * r + 2] = qa.z;
+                            pr.w[8 * r + 3] = qa.w;
+                            pr.w[8 * r + 4] = qb.x;
+                            pr.w[8 * r + 5] = qb.y;
+                            pr.w[8 * r + 6] = qb.z;
+                            pr.w[8 * r + 7] = qb.w;
+                        }
+                    }
+                    pr.flags = (1u << (2 * Shape::VPL)) - 1u;
+                    return;
+                }
+            }
             pr.flags = 0u;
 #pragma unroll
             for (int r = 0; r < Shape::VPL; ++r) {
