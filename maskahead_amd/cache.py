@@ -465,10 +465,35 @@ class PackedKVCache:
             raise ValueError("compact cannot grow the cache")
         return c
 
+    def _sparse_after(self, c: int) -> bool:
+        """Whether storage holding c entries is mostly empty (then it is given back)."""
+        return self.capacity > 2 * c + 2048
+
     def _shrink_if_sparse(self, c: int) -> None:
         """Give back storage when a compaction left it mostly empty."""
-        if self.capacity > 2 * c + 2048:
+        if self._sparse_after(c):
             self._realloc(tokens=_ceil_to(c + 1024, self.quant.key_token_group))
+
+    def _gather_into_smaller(self, keep2: torch.Tensor, c: int) -> None:
+        """A 16-bit store's compaction that leaves it mostly empty: the kept rows (keep2
+        [L * B, H, c]) gathered by ma_gather_kv straight into smaller planes, one read and
+        one write of each kept row, instead of moving them in place and copying them again
+        into smaller planes.  Every row is copied exactly (16-bit values through f32)."""
+        from .kernels.ops import gather_packed_kv
+        from .kernels.splitk import Prefix
+
+        lb, h, d = self.num_layers * self.batch_size, self.num_kv_heads, self.head_dim
+        rows = _ceil_to(c + 1024, self.quant.key_token_group)
+        old_k, old_v = self.k_fp, self.v_fp
+        src = Prefix.dense(old_k.view(lb, h, old_k.shape[3], d)[:, :, :self.length],
+                           old_v.view(lb, h, old_v.shape[3], d)[:, :, :self.length])
+        new_k = torch.empty((self.num_layers, self.batch_size, h, rows, d), device=self.device, dtype=old_k.dtype)
+        new_v = torch.empty_like(new_k, dtype=old_v.dtype)
+        gather_packed_kv(src, keep2, out_key=new_k.view(lb, h, rows, d)[:, :, :c],
+                         out_value=new_v.view(lb, h, rows, d)[:, :, :c])
+        self.k_fp, self.v_fp = new_k, new_v
+        self.planes_generation += 1
+        self.length = c
 
     def compact(self, keep: torch.Tensor) -> None:
         """Keep only stored entries keep[l, b, h, :] of every layer, in that order; positions
@@ -481,10 +506,12 @@ class PackedKVCache:
         removed = self.length - c
         if not self.quant.packed:
             lb, h = self.num_layers * self.batch_size, self.num_kv_heads
-            planes = [t.view(lb, h, t.shape[3], t.shape[4]) for t in (self.k_fp, self.v_fp)]
-            compact_tokens(planes, keep.reshape(lb, h, c), self.length)
-            self.length = c
-            self._shrink_if_sparse(c)
+            if self._sparse_after(c):
+                self._gather_into_smaller(keep.reshape(lb, h, c), c)
+            else:
+                planes = [t.view(lb, h, t.shape[3], t.shape[4]) for t in (self.k_fp, self.v_fp)]
+                compact_tokens(planes, keep.reshape(lb, h, c), self.length)
+                self.length = c
         else:
             kv = [gather_packed_kv(self.layer_view(layer), keep[layer].to(torch.int64), dtype=self.compute_dtype)
                   for layer in range(self.num_layers)]
